@@ -1,0 +1,114 @@
+"""ctypes binding of libsfa.so (include/sfa.h).
+
+The library is built in-tree by ``strataflow_amd.build``.  Loading fails loudly
+when it is missing: there is no CPU fallback for the attention path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libsfa.so"
+
+SFA_OK = 0
+SFA_ERR_INVALID_ARGUMENT = 1
+SFA_ERR_UNSUPPORTED = 3
+SFA_ERR_OUT_OF_MEMORY = 4
+SFA_ERR_RUNTIME = 7
+
+SFA_KV_F32 = 0
+SFA_KV_F16 = 1
+SFA_KV_Q8_0 = 8
+
+#: every symbol include/sfa.h declares
+EXPORTS = (
+    "sfa_status_str",
+    "sfa_version",
+    "sfa_row_bytes",
+    "sfa_page_bytes",
+    "sfa_kv_desc_check",
+    "sfa_kv_append",
+    "sfa_decode_workspace_bytes",
+    "sfa_workspace_init",
+    "sfa_attn_decode",
+    "sfa_attn_prefill",
+    "sfa_page_table_check",
+)
+
+
+class SfaKvDesc(ctypes.Structure):
+    _fields_ = [
+        ("n_head", ctypes.c_int32),
+        ("n_head_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("kv_type", ctypes.c_int32),
+        ("n_pages", ctypes.c_int32),
+        ("k_pages", ctypes.c_void_p),
+        ("v_pages", ctypes.c_void_p),
+        ("n_cold_pages", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("k_cold", ctypes.c_void_p),
+        ("v_cold", ctypes.c_void_p),
+    ]
+
+
+class SfaError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {status_str(status)} ({status})")
+
+
+_lib = None
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Loads libsfa.so (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = Path(path or os.environ.get("SFA_LIB", LIB_PATH))
+    if not p.exists():
+        raise RuntimeError(
+            f"{p} is missing: build the HIP library first "
+            "(python -m strataflow_amd.build); there is no CPU fallback"
+        )
+    lib = ctypes.CDLL(str(p))
+    P = ctypes.c_void_p
+    i32 = ctypes.c_int32
+    D = ctypes.POINTER(SfaKvDesc)
+    lib.sfa_status_str.argtypes = [ctypes.c_int]
+    lib.sfa_status_str.restype = ctypes.c_char_p
+    lib.sfa_version.argtypes = []
+    lib.sfa_version.restype = ctypes.c_char_p
+    lib.sfa_row_bytes.argtypes = [D]
+    lib.sfa_row_bytes.restype = ctypes.c_size_t
+    lib.sfa_page_bytes.argtypes = [D]
+    lib.sfa_page_bytes.restype = ctypes.c_size_t
+    lib.sfa_kv_desc_check.argtypes = [D]
+    lib.sfa_kv_desc_check.restype = ctypes.c_int
+    lib.sfa_kv_append.argtypes = [D, P, P, P, P, i32, P, i32, P]
+    lib.sfa_kv_append.restype = ctypes.c_int
+    lib.sfa_decode_workspace_bytes.argtypes = [D, i32, i32]
+    lib.sfa_decode_workspace_bytes.restype = ctypes.c_size_t
+    lib.sfa_workspace_init.argtypes = [P, ctypes.c_size_t, P]
+    lib.sfa_workspace_init.restype = ctypes.c_int
+    lib.sfa_attn_decode.argtypes = [D, P, P, P, i32, P, P, i32, i32, ctypes.c_float, P,
+                                    ctypes.c_size_t, P]
+    lib.sfa_attn_decode.restype = ctypes.c_int
+    lib.sfa_attn_prefill.argtypes = [D, P, P, P, i32, i32, i32, i32, ctypes.c_float, P]
+    lib.sfa_attn_prefill.restype = ctypes.c_int
+    lib.sfa_page_table_check.argtypes = [D, P, i32, P, P, i32]
+    lib.sfa_page_table_check.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def status_str(status: int) -> str:
+    return load().sfa_status_str(int(status)).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != SFA_OK:
+        raise SfaError(status, what)

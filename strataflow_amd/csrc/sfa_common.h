@@ -1,0 +1,56 @@
+// sfa_common.h - shared device/host helpers of the gfx950 paged-KV attention
+// library.  Wave64 only (CDNA4); no other target is built.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sfa.h"
+
+namespace sfa {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+constexpr int kTile = 32;    // positions per wave tile in decode
+constexpr int kQK = 32;      // Q8_0 block length
+constexpr int kQ8Bytes = 34; // sizeof(block_q8_0)
+
+// Row bytes of one (position, kv head) row for a cache type; 0 if unsupported.
+__host__ __device__ inline int row_bytes_of(int kv_type, int head_dim) {
+    switch (kv_type) {
+    case SFA_KV_F16: return head_dim * 2;
+    case SFA_KV_Q8_0: return (head_dim / kQK) * kQ8Bytes;
+    default: return 0;
+    }
+}
+
+// Resolves a page-table entry to the base address of that page in the device
+// pool (id >= 0) or the cold pool (id <= -2).  Returns nullptr for -1 or an id
+// outside the pool, so a bad table never turns into an out-of-bounds read.
+__device__ inline const uint8_t *page_base(int32_t id, const uint8_t *pool, int n_pages,
+                                           const uint8_t *cold, int n_cold,
+                                           int64_t page_bytes) {
+    if (id >= 0) {
+        if (id >= n_pages || pool == nullptr) return nullptr;
+        return pool + (int64_t)id * page_bytes;
+    }
+    if (id <= -2) {
+        const int64_t c = -2 - (int64_t)id;
+        if (c >= n_cold || cold == nullptr) return nullptr;
+        return cold + c * page_bytes;
+    }
+    return nullptr;
+}
+
+// Cross-half exchange: value of lane (l ^ 32).
+__device__ inline float xor32(float x) {
+    return __shfl_xor(x, 32, 64);
+}
+
+}  // namespace sfa

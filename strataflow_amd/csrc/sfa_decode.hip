@@ -1,0 +1,411 @@
+// sfa_decode.hip - split-K paged decode attention for gfx950 (f16 KV).
+//
+// Replaces kq = mul_mat(k, q) -> soft_max_ext(kq, 0-mask, scale) -> mul_mat(vt, kq)
+// of build_kv_attention (src/model/engine/engine.cpp:1751-1761) for one query
+// token per sequence.  One workgroup = (sequence b, kv head, split s); its four
+// waves walk 32-position tiles of the split.  Per tile a wave
+//   - loads the 32 K rows straight into the A operand of v_mfma_f32_32x32x16_f16
+//     (lane = position, 8 consecutive dims per lane, 16-byte loads),
+//   - computes S^T = K * Q^T on MFMA.  Q^T's 32 columns hold the g query heads of
+//     this kv head replicated (column n is head n % g), so every lane owns the
+//     scores of its column's head for 16 positions and the softmax needs no
+//     cross-lane traffic except one lane^32 max,
+//   - runs an fp32 online softmax in the log2 domain,
+//   - keeps P in registers as the B operand of O^T = V^T * P^T (the MFMA output
+//     layout of S^T is exactly the B layout P^T needs),
+//   - stages the V tile through LDS (coalesced 16-byte loads in, transposed
+//     2-byte gathers out) to build the V^T operand.
+// Waves merge through LDS; splits merge in the same launch: each workgroup
+// stores (m, l, o) to the workspace and the last one to arrive for a
+// (sequence, kv head) merges all splits in split order, so the result does not
+// depend on arrival order or page placement.
+#include "sfa_common.h"
+
+namespace sfa {
+
+struct DecodeParams {
+    const uint8_t *k_pages;
+    const uint8_t *v_pages;
+    const uint8_t *k_cold;
+    const uint8_t *v_cold;
+    int64_t page_bytes;
+    int n_pages;
+    int n_cold;
+    int page_size;
+    int n_head_kv;
+    int n_head;
+    int row_bytes;
+    const float *q;
+    float *out;
+    const int32_t *page_table;
+    int max_pages;
+    const int32_t *seq_len;
+    const int32_t *kv_lo;
+    int n_splits;         // grid.x
+    int tiles_per_split;  // minimum tiles per split (host heuristic)
+    float scale_log2;     // scale * log2(e)
+    float *part;          // [B][Hkv][n_splits][G][HD + 4]
+    uint32_t *counters;   // [B][Hkv]
+};
+
+constexpr int kDecodeWaves = 4;
+
+// Active tile range of sequence b: tiles are 32-aligned absolute position
+// blocks [32t, 32t+32) intersecting [lo, n_kv).
+__device__ inline void seq_tiles(const DecodeParams &p, int b, int &lo, int &n_kv, int &t0,
+                                 int &n_tiles, int &tps, int &n_active) {
+    n_kv = p.seq_len[b];
+    const int cap = p.max_pages * p.page_size;
+    if (n_kv > cap) n_kv = cap;
+    lo = p.kv_lo ? p.kv_lo[b] : 0;
+    if (lo < 0) lo = 0;
+    if (n_kv <= lo) {
+        t0 = 0; n_tiles = 0; tps = 1; n_active = 0;
+        return;
+    }
+    t0 = lo / kTile;
+    n_tiles = (n_kv + kTile - 1) / kTile - t0;
+    tps = p.tiles_per_split;
+    const int need = (n_tiles + p.n_splits - 1) / p.n_splits;
+    if (tps < need) tps = need;
+    n_active = (n_tiles + tps - 1) / tps;
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
+    static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
+    static_assert(G >= 1 && G <= 32 && (32 % G) == 0, "group size");
+    constexpr int KC = HD / 16;          // 16-dim k chunks of the QK MFMA
+    constexpr int DB = HD / 32;          // 32-dim blocks of the PV MFMA output
+    constexpr int VROW = HD * 2 + 16;    // padded LDS row of the V tile (bytes)
+    constexpr int CPR = HD / 8;          // 16-byte chunks per row
+    constexpr int RPI = kWave / CPR;     // rows per coalesced V load
+    constexpr int VIT = kTile / RPI;     // V loads per lane per tile
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[kDecodeWaves][kTile * VROW];
+    __shared__ float lds_m[kDecodeWaves][G];
+    __shared__ float lds_l[kDecodeWaves][G];
+    __shared__ float lds_o[kDecodeWaves][G][HD];
+    __shared__ float lds_w[256];
+    __shared__ int lds_last;
+
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 31;   // MFMA column (head replica) / A-operand row
+    const int hh = lane >> 5;  // k half
+
+    int lo, n_kv, t0, n_tiles, tps, n_active;
+    seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
+    const int Hkv = p.n_head_kv;
+    float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
+    if (split >= n_active) {
+        if (split == 0 && n_active == 0) {
+            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out_b[i] = 0.0f;
+        }
+        return;
+    }
+
+    // Q^T operand: column n -> head kvh*G + n%G, dims 16c + 8hh .. +8, f16
+    // (the F16 vec_dot_type conversion ggml applies to src1).
+    half8 qf[KC];
+    {
+        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G + (n % G)) * HD;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 16 * c + 8 * hh);
+            const floatx4 x0 = src[0], x1 = src[1];
+            half8 h;
+            h[0] = (_Float16)x0[0]; h[1] = (_Float16)x0[1]; h[2] = (_Float16)x0[2]; h[3] = (_Float16)x0[3];
+            h[4] = (_Float16)x1[0]; h[5] = (_Float16)x1[1]; h[6] = (_Float16)x1[2]; h[7] = (_Float16)x1[3];
+            qf[c] = h;
+        }
+    }
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+
+    const int tile_lo = t0 + split * tps;
+    int tile_hi = tile_lo + tps;
+    if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
+    const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
+    const int32_t *pt = p.page_table + (int64_t)b * p.max_pages;
+    uint8_t *vt = lds_v[wave];
+
+    for (int t = tile_lo + wave; t < tile_hi; t += kDecodeWaves) {
+        const int pos0 = t * kTile;
+        const int lpage = pos0 / p.page_size;
+        const int32_t pid = pt[lpage];
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        if (kb == nullptr || vb == nullptr) continue;  // invalid page: tile contributes nothing
+        const int64_t off0 = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
+
+        // K rows into the A operand: row n, dims 16c + 8hh.
+        const int kpos = pos0 + n;
+        const bool kvalid = kpos >= lo && kpos < n_kv;
+        half8 kf[KC];
+        {
+            const uint8_t *kr = kb + off0 + (int64_t)n * col_bytes + 16 * hh;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                kf[c] = kvalid ? *reinterpret_cast<const half8 *>(kr + 32 * c) : half8{};
+            }
+        }
+        // V rows, coalesced: row r = i*RPI + lane/CPR, chunk lane%CPR.
+        half8 vr[VIT];
+#pragma unroll
+        for (int i = 0; i < VIT; ++i) {
+            const int r = i * RPI + lane / CPR;
+            const int vpos = pos0 + r;
+            const bool vvalid = vpos >= lo && vpos < n_kv;
+            const uint8_t *src = vb + off0 + (int64_t)r * col_bytes + 16 * (lane % CPR);
+            vr[i] = vvalid ? *reinterpret_cast<const half8 *>(src) : half8{};
+        }
+
+        // S^T = K * Q^T
+        floatx16 s = floatx16{};
+#pragma unroll
+        for (int c = 0; c < KC; ++c) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s, 0, 0, 0);
+
+        // V tile into LDS (wave-private region) while the MFMAs drain.
+#pragma unroll
+        for (int i = 0; i < VIT; ++i) {
+            const int r = i * RPI + lane / CPR;
+            *reinterpret_cast<half8 *>(vt + r * VROW + 16 * (lane % CPR)) = vr[i];
+        }
+
+        // online softmax (log2 domain); row of register i is position
+        // 8(i/4) + 4hh + i%4 of the tile.
+        float sv[16];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i >> 2) + 4 * hh + (i & 3);
+            const int pp = pos0 + r;
+            const bool ok = pp >= lo && pp < n_kv;
+            sv[i] = ok ? s[i] * p.scale_log2 : -INFINITY;
+            mt = fmaxf(mt, sv[i]);
+        }
+        mt = fmaxf(mt, xor32(mt));
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = exp2f(m_run - m_new);
+        float ls = 0.0f;
+        half8 pb[2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float e = exp2f(sv[i] - m_new);
+            ls += e;
+            pb[i >> 3][i & 7] = (_Float16)e;
+        }
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) o[d] *= alpha;
+
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // O^T += V^T * P^T; k index 8hh + j of chunk kk is tile position
+        // 16kk + 8(j/4) + 4hh + j%4 (the rows this lane holds in pb[kk]).
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                half8 a;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int r = 16 * kk + 8 * (j >> 2) + 4 * hh + (j & 3);
+                    a[j] = *reinterpret_cast<const _Float16 *>(vt + r * VROW + 2 * (32 * d + n));
+                }
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kk], o[d], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // wave partial -> LDS (column n < G is head n; dims of register i of block
+    // d are 32d + 8(i/4) + 4hh + i%4)
+    l_run += xor32(l_run);
+    if (n < G) {
+        if (hh == 0) {
+            lds_m[wave][n] = m_run;
+            lds_l[wave][n] = l_run;
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                lds_o[wave][n][32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i];
+            }
+        }
+    }
+    __syncthreads();
+
+    // merge the waves; the workgroup's (m, l, o) per head
+    const int64_t head_base = (int64_t)b * Hkv + kvh;
+    float *part = p.part + (head_base * p.n_splits + split) * G * (HD + 4);
+    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
+        const int g = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, lds_m[w][g]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            const float mw = lds_m[w][g];
+            const float wt = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+            L += lds_l[w][g] * wt;
+            O += lds_o[w][g][d] * wt;
+        }
+        if (n_active == 1) {
+            out_b[g * HD + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            part[g * (HD + 4) + d] = O;
+            if (d == 0) {
+                part[g * (HD + 4) + HD] = M;
+                part[g * (HD + 4) + HD + 1] = L;
+            }
+        }
+    }
+    if (n_active == 1) return;
+
+    // last arriver merges the splits
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(&p.counters[head_base], 1u);
+        lds_last = (prev == (uint32_t)(n_active - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!lds_last) return;
+    __threadfence();
+    const float *pbase = p.part + head_base * p.n_splits * G * (HD + 4);
+    for (int g = 0; g < G; ++g) {
+        float M = -INFINITY;
+        for (int s = threadIdx.x; s < n_active; s += blockDim.x)
+            M = fmaxf(M, pbase[((int64_t)s * G + g) * (HD + 4) + HD]);
+        // block max
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        if (lane == 0) lds_w[wave] = M;
+        __syncthreads();
+        M = fmaxf(fmaxf(lds_w[0], lds_w[1]), fmaxf(lds_w[2], lds_w[3]));
+        __syncthreads();
+        for (int d = threadIdx.x; d < HD; d += blockDim.x) {
+            float L = 0.0f, O = 0.0f;
+            for (int s = 0; s < n_active; ++s) {
+                const float *ps = pbase + ((int64_t)s * G + g) * (HD + 4);
+                const float wt = ps[HD] == -INFINITY ? 0.0f : exp2f(ps[HD] - M);
+                L += ps[HD + 1] * wt;
+                O += ps[d] * wt;
+            }
+            out_b[g * HD + d] = L > 0.0f ? O / L : 0.0f;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) p.counters[head_base] = 0u;
+}
+
+// ---- host side -------------------------------------------------------------
+
+struct SplitPlan {
+    int n_splits;
+    int tiles_per_split;
+};
+
+SplitPlan plan_splits(int B, int Hkv, int max_seq_len) {
+    const int tiles = (max_seq_len + kTile - 1) / kTile + 1;
+    const int heads = B * Hkv;
+    const int wg_target = 1024;
+    int S = (wg_target + heads - 1) / heads;
+    if (S < 1) S = 1;
+    if (S > 256) S = 256;
+    int tps = (tiles + S - 1) / S;
+    if (tps < kDecodeWaves) tps = kDecodeWaves;
+    S = (tiles + tps - 1) / tps;
+    if (S < 1) S = 1;
+    return SplitPlan{S, tps};
+}
+
+size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
+    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len);
+    const size_t counters = ((size_t)B * Hkv * sizeof(uint32_t) + 255) & ~(size_t)255;
+    const size_t part = (size_t)B * Hkv * sp.n_splits * G * (HD + 4) * sizeof(float);
+    return counters + part;
+}
+
+template <int HD, int G>
+static void launch_f16(const DecodeParams &p, int B, int Hkv, hipStream_t s) {
+    dim3 grid(p.n_splits, Hkv, B);
+    hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
+}
+
+template <int HD>
+static int launch_f16_g(const DecodeParams &p, int G, int B, int Hkv, hipStream_t s) {
+    switch (G) {
+    case 1: launch_f16<HD, 1>(p, B, Hkv, s); return SFA_OK;
+    case 2: launch_f16<HD, 2>(p, B, Hkv, s); return SFA_OK;
+    case 4: launch_f16<HD, 4>(p, B, Hkv, s); return SFA_OK;
+    case 8: launch_f16<HD, 8>(p, B, Hkv, s); return SFA_OK;
+    default: return SFA_ERR_UNSUPPORTED;
+    }
+}
+
+int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
+                  int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                  int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
+                  hipStream_t stream) {
+    const int Hkv = kv->n_head_kv, HD = kv->head_dim, G = kv->n_head / kv->n_head_kv;
+    if (B <= 0 || max_seq_len <= 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
+    if (q == nullptr || out == nullptr || page_table == nullptr || seq_len == nullptr)
+        return SFA_ERR_INVALID_ARGUMENT;
+    const size_t need = decode_workspace_bytes(B, Hkv, G, HD, max_seq_len);
+    if (workspace == nullptr || ws_bytes < need) return SFA_ERR_INVALID_ARGUMENT;
+    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len);
+    const size_t counters = ((size_t)B * Hkv * sizeof(uint32_t) + 255) & ~(size_t)255;
+
+    DecodeParams p;
+    p.k_pages = static_cast<const uint8_t *>(kv->k_pages);
+    p.v_pages = static_cast<const uint8_t *>(kv->v_pages);
+    p.k_cold = static_cast<const uint8_t *>(kv->k_cold);
+    p.v_cold = static_cast<const uint8_t *>(kv->v_cold);
+    p.row_bytes = row_bytes_of(kv->kv_type, HD);
+    p.page_bytes = (int64_t)p.row_bytes * Hkv * kv->page_size;
+    p.n_pages = kv->n_pages;
+    p.n_cold = kv->n_cold_pages;
+    p.page_size = kv->page_size;
+    p.n_head_kv = Hkv;
+    p.n_head = kv->n_head;
+    p.q = q;
+    p.out = out;
+    p.page_table = page_table;
+    p.max_pages = max_pages;
+    p.seq_len = seq_len;
+    p.kv_lo = kv_lo;
+    p.n_splits = sp.n_splits;
+    p.tiles_per_split = sp.tiles_per_split;
+    p.scale_log2 = scale * 1.4426950408889634f;
+    p.counters = static_cast<uint32_t *>(workspace);
+    p.part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + counters);
+
+    if (kv->kv_type != SFA_KV_F16) return SFA_ERR_UNSUPPORTED;
+    int rc;
+    switch (HD) {
+    case 32: rc = launch_f16_g<32>(p, G, B, Hkv, stream); break;
+    case 64: rc = launch_f16_g<64>(p, G, B, Hkv, stream); break;
+    case 128: rc = launch_f16_g<128>(p, G, B, Hkv, stream); break;
+    default: return SFA_ERR_UNSUPPORTED;
+    }
+    if (rc != SFA_OK) return rc;
+    return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+}
+
+}  // namespace sfa

@@ -1,0 +1,258 @@
+// sfa_prefill.hip - chunked causal prefill attention over the paged f16 cache.
+//
+// The same op sequence as build_kv_attention (src/model/engine/engine.cpp:
+// 1751-1761) for T query tokens of one sequence, with llama.cpp's causal mask
+// (-INF where kv position > query position).  The reference engine itself only
+// issues T == 1 (engine.cpp:2796); this is the chunked extension.
+//
+// One workgroup = (query block, kv head); its 128 MFMA rows are the g query
+// heads of that kv head times 128/g query tokens, so every K/V tile read from
+// the cache serves all g heads.  Per 64-position tile the four waves share a K
+// tile and a V tile in LDS; each wave computes S^T = K * Q^T on
+// v_mfma_f32_32x32x16_f16 (K rows from LDS, Q^T in registers), runs an fp32
+// online softmax in the log2 domain with the lane owning its query row, and
+// accumulates O^T += V^T * P^T (P^T straight from the S^T accumulator layout).
+// Tiles above the block's last query position are never visited.
+#include "sfa_common.h"
+
+namespace sfa {
+
+struct PrefillParams {
+    const uint8_t *k_pages;
+    const uint8_t *v_pages;
+    const uint8_t *k_cold;
+    const uint8_t *v_cold;
+    int64_t page_bytes;
+    int n_pages;
+    int n_cold;
+    int page_size;
+    int n_head_kv;
+    int n_head;
+    const float *q;
+    float *out;
+    const int32_t *page_table;
+    int max_pages;
+    int q_pos0;
+    int T;
+    int kv_lo;
+    int n_qblk;
+    float scale_log2;
+};
+
+constexpr int kPBN = 64;           // positions per prefill tile
+
+template <int HD, int G>
+__global__ __launch_bounds__(256) void prefill_f16_kernel(PrefillParams p) {
+    constexpr int KC = HD / 16;
+    constexpr int DB = HD / 32;
+    constexpr int QB = 128 / G;           // query tokens per workgroup
+    constexpr int ROW = HD * 2 + 16;      // padded LDS row (bytes)
+    constexpr int CPR = HD / 8;           // 16-byte chunks per row
+    constexpr int CHUNKS = kPBN * CPR;    // 16-byte chunks per tile
+    constexpr int LPT = CHUNKS / 256;     // chunks per thread per tile
+    static_assert(CHUNKS % 256 == 0, "tile chunks");
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k[kPBN * ROW];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[kPBN * ROW];
+
+    const int qblk = p.n_qblk - 1 - (int)blockIdx.x;  // heaviest blocks first
+    const int kvh = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+    const int Hkv = p.n_head_kv;
+    const int64_t col_bytes = (int64_t)Hkv * HD * 2;
+
+    // this lane's query row
+    const int rho = wave * 32 + n;
+    const int g = rho / QB;
+    const int tq = qblk * QB + rho % QB;
+    const bool row_ok = tq < p.T;
+    const int h = kvh * G + g;
+    const int qp = p.q_pos0 + tq;
+
+    half8 qf[KC];
+    {
+        const float *qr = p.q + ((int64_t)(row_ok ? tq : 0) * p.n_head + h) * HD;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            half8 hv;
+            if (row_ok) {
+                const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 16 * c + 8 * hh);
+                const floatx4 x0 = src[0], x1 = src[1];
+                hv[0] = (_Float16)x0[0]; hv[1] = (_Float16)x0[1]; hv[2] = (_Float16)x0[2]; hv[3] = (_Float16)x0[3];
+                hv[4] = (_Float16)x1[0]; hv[5] = (_Float16)x1[1]; hv[6] = (_Float16)x1[2]; hv[7] = (_Float16)x1[3];
+            } else {
+                hv = half8{};
+            }
+            qf[c] = hv;
+        }
+    }
+
+    // the block's kv range
+    int last_tok = (qblk + 1) * QB - 1;
+    if (last_tok > p.T - 1) last_tok = p.T - 1;
+    const int kv_hi = p.q_pos0 + last_tok;     // inclusive
+    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
+    const int tile0 = lo / kPBN;
+    const int tile1 = kv_hi / kPBN;             // inclusive
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    for (int t = tile0; t <= tile1; ++t) {
+        const int pos0 = t * kPBN;
+        // cooperative tile load: chunk id = i*256 + tid -> row = id / CPR
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int id = i * 256 + threadIdx.x;
+            const int r = id / CPR, c = id % CPR;
+            const int pp = pos0 + r;
+            half8 kv8 = half8{}, vv8 = half8{};
+            if (pp >= lo && pp <= kv_hi) {
+                const int lp = pp / p.page_size;
+                const int32_t pid = lp < p.max_pages ? p.page_table[lp] : -1;
+                const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+                const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+                const int64_t off = (int64_t)(pp - lp * p.page_size) * col_bytes + (int64_t)kvh * HD * 2 + 16 * c;
+                if (kb) kv8 = *reinterpret_cast<const half8 *>(kb + off);
+                if (vb) vv8 = *reinterpret_cast<const half8 *>(vb + off);
+            }
+            *reinterpret_cast<half8 *>(lds_k + r * ROW + 16 * c) = kv8;
+            *reinterpret_cast<half8 *>(lds_v + r * ROW + 16 * c) = vv8;
+        }
+        __syncthreads();
+
+        float sv[2][16];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+            floatx16 s = floatx16{};
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                const half8 a = *reinterpret_cast<const half8 *>(lds_k + (32 * pb + n) * ROW + 32 * c + 16 * hh);
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
+                const bool ok = row_ok && kp >= lo && kp <= qp;
+                sv[pb][i] = ok ? s[i] * p.scale_log2 : -INFINITY;
+                mt = fmaxf(mt, sv[pb][i]);
+            }
+        }
+        mt = fmaxf(mt, xor32(mt));
+        const float m_new = fmaxf(m_run, mt);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = exp2f(m_run - m_use);
+        m_run = m_new;
+        float ls = 0.0f;
+        half8 pbv[2][2];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float e = exp2f(sv[pb][i] - m_use);
+                ls += e;
+                pbv[pb][i >> 3][i & 7] = (_Float16)e;
+            }
+        }
+        l_run = l_run * alpha + ls;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) o[d] *= alpha;
+
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+                    half8 a;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int r = 32 * pb + 16 * kk + 8 * (j >> 2) + 4 * hh + (j & 3);
+                        a[j] = *reinterpret_cast<const _Float16 *>(lds_v + r * ROW + 2 * (32 * d + n));
+                    }
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pbv[pb][kk], o[d], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    l_run += xor32(l_run);
+    if (row_ok) {
+        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+        float *orow = p.out + ((int64_t)tq * p.n_head + h) * HD;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                orow[32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i] * inv;
+            }
+        }
+    }
+}
+
+template <int HD, int G>
+static void launch_prefill(const PrefillParams &p, hipStream_t s) {
+    hipLaunchKernelGGL((prefill_f16_kernel<HD, G>), dim3(p.n_qblk, p.n_head_kv), dim3(256), 0, s, p);
+}
+
+template <int HD>
+static int launch_prefill_g(const PrefillParams &p, int G, hipStream_t s) {
+    switch (G) {
+    case 1: launch_prefill<HD, 1>(p, s); return SFA_OK;
+    case 2: launch_prefill<HD, 2>(p, s); return SFA_OK;
+    case 4: launch_prefill<HD, 4>(p, s); return SFA_OK;
+    case 8: launch_prefill<HD, 8>(p, s); return SFA_OK;
+    default: return SFA_ERR_UNSUPPORTED;
+    }
+}
+
+int prefill_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
+                   int32_t max_pages, int32_t q_pos0, int32_t T, int32_t kv_lo, float scale,
+                   hipStream_t stream) {
+    if (kv->kv_type != SFA_KV_F16) return SFA_ERR_UNSUPPORTED;
+    if (kv->page_size % kPBN != 0) return SFA_ERR_UNSUPPORTED;
+    if (q == nullptr || out == nullptr || page_table == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+    if (T < 0 || q_pos0 < 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
+    if (T == 0) return SFA_OK;
+    if ((int64_t)q_pos0 + T > (int64_t)max_pages * kv->page_size) return SFA_ERR_INVALID_ARGUMENT;
+    const int G = kv->n_head / kv->n_head_kv;
+    PrefillParams p;
+    p.k_pages = static_cast<const uint8_t *>(kv->k_pages);
+    p.v_pages = static_cast<const uint8_t *>(kv->v_pages);
+    p.k_cold = static_cast<const uint8_t *>(kv->k_cold);
+    p.v_cold = static_cast<const uint8_t *>(kv->v_cold);
+    p.page_bytes = (int64_t)kv->head_dim * 2 * kv->n_head_kv * kv->page_size;
+    p.n_pages = kv->n_pages;
+    p.n_cold = kv->n_cold_pages;
+    p.page_size = kv->page_size;
+    p.n_head_kv = kv->n_head_kv;
+    p.n_head = kv->n_head;
+    p.q = q;
+    p.out = out;
+    p.page_table = page_table;
+    p.max_pages = max_pages;
+    p.q_pos0 = q_pos0;
+    p.T = T;
+    p.kv_lo = kv_lo;
+    const int QB = 128 / G;
+    p.n_qblk = (T + QB - 1) / QB;
+    p.scale_log2 = scale * 1.4426950408889634f;
+    int rc;
+    switch (kv->head_dim) {
+    case 32: rc = launch_prefill_g<32>(p, G, stream); break;
+    case 64: rc = launch_prefill_g<64>(p, G, stream); break;
+    case 128: rc = launch_prefill_g<128>(p, G, stream); break;
+    default: return SFA_ERR_UNSUPPORTED;
+    }
+    if (rc != SFA_OK) return rc;
+    return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+}
+
+}  // namespace sfa

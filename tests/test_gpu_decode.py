@@ -1,0 +1,128 @@
+"""Decode attention on the GPU (sfa_attn_decode through the C ABI) against the
+oracle: ggml CPU semantics (max-abs <= 2e-3, rel-L2 <= 1e-3) and float64."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.helpers import Case, assert_close, errors, f16_cols, golden, scatter_columns
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("name", ["attn_f16_gqa2_decode", "attn_f16_gqa4_window"])
+def test_decode_golden(gpu, oracle_mod, name):
+    import torch
+    from strataflow_amd.paged_kv import PagedKV
+    g = golden(name)
+    n_kv, Hkv, hd = g["k_f16"].shape
+    Hq = int(g["n_head"])
+    ps, n_pages = 32, (n_kv + 31) // 32 + 3
+    kp, pt = scatter_columns(f16_cols(g["k_f16"]), ps, n_pages, np.random.default_rng(1))
+    vp, _ = scatter_columns(f16_cols(g["v_f16"]), ps, n_pages, np.random.default_rng(1))
+    dev = PagedKV(1, Hq, Hkv, hd, 1, ps, n_pages, device=gpu)
+    dev.k[0].copy_(torch.from_numpy(kp))
+    dev.v[0].copy_(torch.from_numpy(vp))
+    q = torch.from_numpy(g["q"]).to(gpu)  # [1, Hq, hd]
+    lo = torch.tensor([int(g["kv_lo"])], dtype=torch.int32, device=gpu)
+    out = dev.decode(0, q, torch.from_numpy(pt).to(gpu), torch.tensor([n_kv], dtype=torch.int32, device=gpu),
+                     n_kv, kv_lo=lo, scale=float(g["scale"]))
+    out = out.cpu().numpy().reshape(g["exact"].shape)
+    assert_close(out, g["ggml"], what="vs ggml golden")
+    assert_close(out, g["exact"], what="vs exact golden")
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128), (8, 4, 32), (8, 8, 64), (16, 2, 128), (16, 16, 128)])
+@pytest.mark.parametrize("n_kv", [1, 31, 33, 257, 1000])
+def test_decode_shapes(gpu, oracle_mod, shape, n_kv):
+    Hq, Hkv, hd = shape
+    c = Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, page_size=64,
+             seed=n_kv + hd)
+    out = c.decode()
+    assert_close(out, c.oracle(oracle_mod.GGML), what=f"{shape} n_kv={n_kv} vs ggml")
+    assert_close(out, c.oracle(oracle_mod.EXACT), what=f"{shape} n_kv={n_kv} vs exact")
+
+
+def test_decode_mixtral_ctx4096(gpu, oracle_mod):
+    # Mixtral attention shape at context 4096, 256-token pages shuffled
+    c = Case(oracle_mod, seq_lens=[4096], seed=42)
+    out = c.decode()
+    ma, rl = assert_close(out, c.oracle(oracle_mod.GGML), what="ctx4096 vs ggml")
+    print(f"ctx4096 f16: max_abs {ma:.3e} rel_l2 {rl:.3e}")
+    assert_close(out, c.oracle(oracle_mod.EXACT), what="ctx4096 vs exact")
+
+
+def test_decode_batch_varlen_window(gpu, oracle_mod):
+    # B=5 sequences sharing one pool, different lengths; two use a sliding
+    # window start (kv_lo), one is empty (all masked -> zeros)
+    seq = [700, 1, 4096, 300, 0]
+    lo = [0, 0, 3000, 290, 0]
+    c = Case(oracle_mod, seq_lens=seq, kv_lo=lo, seed=7)
+    out = c.decode(max_seq_len=4096)
+    ref = c.oracle(oracle_mod.GGML)
+    assert_close(out, ref, what="varlen vs ggml")
+    assert np.all(out[4] == 0)
+
+
+def test_decode_page_placement_bit_identical(gpu, oracle_mod):
+    # paged == contiguous, bit for bit (the reference's test_kv_paging.cpp:243
+    # invariant): same logical cache, different physical page orders
+    import torch
+    c = Case(oracle_mod, seq_lens=[2000], seed=9, extra_pages=6)
+    base = c.decode()
+    n_pages = c.n_pages
+    for seed in (1, 2):
+        perm = np.random.default_rng(seed).permutation(n_pages).astype(np.int32)
+        # move every physical page p to perm[p]
+        k2 = torch.empty_like(c.dev.k[0])
+        v2 = torch.empty_like(c.dev.v[0])
+        k2[torch.from_numpy(perm).long().to(gpu)] = c.dev.k[0]
+        v2[torch.from_numpy(perm).long().to(gpu)] = c.dev.v[0]
+        c.dev.k[0].copy_(k2)
+        c.dev.v[0].copy_(v2)
+        pt = c.page_table.copy()
+        valid = pt >= 0
+        pt[valid] = perm[pt[valid]]
+        c.page_table = pt
+        c.t_pt = torch.from_numpy(pt).to(gpu)
+        out = c.decode()
+        assert np.array_equal(out.view(np.uint32), base.view(np.uint32))
+
+
+def test_decode_deterministic_and_workspace_reuse(gpu, oracle_mod):
+    c = Case(oracle_mod, seq_lens=[3000, 1500], seed=11)
+    a = c.decode()
+    b = c.decode()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # a smaller call on the same (grown) workspace, then the big one again
+    small = Case(oracle_mod, seq_lens=[100], seed=12)
+    small.dev._ws = c.dev._ws
+    assert_close(small.decode(), small.oracle(oracle_mod.GGML), what="small after big")
+    assert np.array_equal(c.decode().view(np.uint32), a.view(np.uint32))
+
+
+def test_decode_bad_page_id_skipped(gpu, oracle_mod):
+    # an out-of-pool page id is caught by the kernel's own bounds check: that
+    # tile contributes nothing and nothing is read out of bounds
+    import torch
+    c = Case(oracle_mod, seq_lens=[600], page_size=256, seed=13)
+    pt = c.page_table.copy()
+    pt[0, 1] = c.n_pages + 100
+    c.t_pt = torch.from_numpy(pt).to(gpu)
+    out = c.decode()
+    assert np.all(np.isfinite(out))
+
+
+def test_decode_rejects_small_workspace(gpu, oracle_mod):
+    import ctypes
+    import torch
+    from strataflow_amd import _lib
+    c = Case(oracle_mod, seq_lens=[100], seed=14)
+    lib = _lib.load()
+    d = c.dev.desc(0)
+    out = torch.empty((1, 32 * 128), device=gpu)
+    ws = torch.zeros(16, dtype=torch.uint8, device=gpu)
+    rc = lib.sfa_attn_decode(ctypes.byref(d), c.t_q.data_ptr(), out.data_ptr(), c.t_pt.data_ptr(),
+                             c.max_pages, c.t_sl.data_ptr(), None, 1, 100, 0.088, ws.data_ptr(), 16,
+                             torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.SFA_ERR_INVALID_ARGUMENT
