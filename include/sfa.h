@@ -100,10 +100,9 @@ SFA_API int sfa_kv_desc_check(const sfa_kv_desc *kv);
  * belongs to sequence seq[i] at absolute position pos[i]; its row lands in
  * page page_table[seq[i] * max_pages + pos[i] / page_size].  F16 caches round
  * to nearest even; Q8_0 caches quantise each 32-block with d = amax/127 (fp16)
- * and q = round(x / d).  Tokens whose page id is -1 or out of range are not
- * written; the call then returns SFA_ERR_INVALID_ARGUMENT after the launch only
- * if the host can see it, so callers validate page tables with
- * sfa_page_table_check(). */
+ * and q = round(x / d).  The kernel writes nothing for a token whose page id
+ * is -1 or outside its pool (it cannot report that back without a sync), so
+ * callers validate host page tables with sfa_page_table_check(). */
 SFA_API int sfa_kv_append(const sfa_kv_desc *kv, const float *k, const float *v,
                           const int32_t *seq, const int32_t *pos, int32_t n_tok,
                           const int32_t *page_table, int32_t max_pages,
@@ -114,9 +113,9 @@ SFA_API int sfa_kv_append(const sfa_kv_desc *kv, const float *k, const float *v,
 SFA_API size_t sfa_decode_workspace_bytes(const sfa_kv_desc *kv, int32_t B,
                                           int32_t max_seq_len);
 
-/* Zeroes a workspace (the split-merge arrival counters must start at zero;
- * every decode call leaves them at zero again).  Uses a fill kernel, so it is
- * safe under stream capture.  Call once after allocating a workspace. */
+/* Zeroes a workspace with a fill kernel (safe under stream capture).  The
+ * decode passes do not need a zeroed workspace; this is for callers that want
+ * deterministic contents before first use. */
 SFA_API int sfa_workspace_init(void *workspace, size_t ws_bytes, void *stream);
 
 /* Decode attention: one query token per sequence (engine.cpp:1751-1761 with
@@ -129,14 +128,32 @@ SFA_API int sfa_workspace_init(void *workspace, size_t ws_bytes, void *stream);
  *           positive kv_lo is an opt-in sliding attention window.
  *   max_seq_len : host bound on every seq_len[b] (sizes the split grid)
  *   scale : 1/sqrt(head_dim) in the reference (engine.cpp:1756)
- * Split-K over logical positions with a fused last-arriver merge: results do
- * not depend on where pages live (paged == contiguous, bit for bit).
+ * Split-K over logical positions, then a merge pass in split order: results
+ * do not depend on where pages live (paged == contiguous, bit for bit).
  * Sequences with seq_len <= kv_lo produce zeros. */
 SFA_API int sfa_attn_decode(const sfa_kv_desc *kv, const float *q, float *out,
                             const int32_t *page_table, int32_t max_pages,
                             const int32_t *seq_len, const int32_t *kv_lo,
                             int32_t B, int32_t max_seq_len, float scale,
                             void *workspace, size_t ws_bytes, void *stream);
+
+/* The two passes of sfa_attn_decode, for callers that schedule them apart
+ * (e.g. to overlap the merge with other work, or to time the split-K pass):
+ * sfa_attn_decode == sfa_attn_decode_split then sfa_attn_decode_merge on the
+ * same stream with the same arguments.  The split pass writes per-split
+ * (m, l, o) partials to the workspace (and the final output directly when a
+ * sequence needs one split); the merge pass combines them.  No counterpart in
+ * the reference: its attention is one ggml graph. */
+SFA_API int sfa_attn_decode_split(const sfa_kv_desc *kv, const float *q, float *out,
+                                  const int32_t *page_table, int32_t max_pages,
+                                  const int32_t *seq_len, const int32_t *kv_lo,
+                                  int32_t B, int32_t max_seq_len, float scale,
+                                  void *workspace, size_t ws_bytes, void *stream);
+SFA_API int sfa_attn_decode_merge(const sfa_kv_desc *kv, const float *q, float *out,
+                                  const int32_t *page_table, int32_t max_pages,
+                                  const int32_t *seq_len, const int32_t *kv_lo,
+                                  int32_t B, int32_t max_seq_len, float scale,
+                                  void *workspace, size_t ws_bytes, void *stream);
 
 /* Chunked causal prefill of ONE sequence: T query tokens at absolute positions
  * q_pos0 .. q_pos0+T-1, whose K/V are already appended.  Token t attends kv

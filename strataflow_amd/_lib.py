@@ -32,6 +32,8 @@ EXPORTS = (
     "sfa_decode_workspace_bytes",
     "sfa_workspace_init",
     "sfa_attn_decode",
+    "sfa_attn_decode_split",
+    "sfa_attn_decode_merge",
     "sfa_attn_prefill",
     "sfa_page_table_check",
 )
@@ -97,6 +99,10 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_attn_decode.argtypes = [D, P, P, P, i32, P, P, i32, i32, ctypes.c_float, P,
                                     ctypes.c_size_t, P]
     lib.sfa_attn_decode.restype = ctypes.c_int
+    for name in ("sfa_attn_decode_split", "sfa_attn_decode_merge"):
+        f = getattr(lib, name)
+        f.argtypes = lib.sfa_attn_decode.argtypes
+        f.restype = ctypes.c_int
     lib.sfa_attn_prefill.argtypes = [D, P, P, P, i32, i32, i32, i32, ctypes.c_float, P]
     lib.sfa_attn_prefill.restype = ctypes.c_int
     lib.sfa_page_table_check.argtypes = [D, P, i32, P, P, i32]

@@ -10,7 +10,7 @@ namespace sfa {
 int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
                   int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
                   int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
-                  hipStream_t stream);
+                  int passes, hipStream_t stream);
 size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len);
 int prefill_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
                    int32_t max_pages, int32_t q_pos0, int32_t T, int32_t kv_lo, float scale,
@@ -98,20 +98,46 @@ SFA_API int sfa_workspace_init(void *workspace, size_t ws_bytes, void *stream) {
     }
 }
 
-SFA_API int sfa_attn_decode(const sfa_kv_desc *kv, const float *q, float *out,
-                            const int32_t *page_table, int32_t max_pages,
-                            const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
-                            int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
-                            void *stream) {
+static int decode_entry(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
+                        int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                        int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
+                        void *stream, int passes) {
     try {
         const int rc = check_desc(kv);
         if (rc != SFA_OK) return rc;
         if (!(scale > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
         return sfa::decode_launch(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len,
-                                  scale, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+                                  scale, workspace, ws_bytes, passes, static_cast<hipStream_t>(stream));
     } catch (...) {
         return SFA_ERR_RUNTIME;
     }
+}
+
+SFA_API int sfa_attn_decode(const sfa_kv_desc *kv, const float *q, float *out,
+                            const int32_t *page_table, int32_t max_pages,
+                            const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                            int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
+                            void *stream) {
+    return decode_entry(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
+                        workspace, ws_bytes, stream, 3);
+}
+
+SFA_API int sfa_attn_decode_split(const sfa_kv_desc *kv, const float *q, float *out,
+                                  const int32_t *page_table, int32_t max_pages,
+                                  const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                                  int32_t max_seq_len, float scale, void *workspace,
+                                  size_t ws_bytes, void *stream) {
+    return decode_entry(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
+                        workspace, ws_bytes, stream, 1);
+}
+
+SFA_API int sfa_attn_decode_merge(const sfa_kv_desc *kv, const float *q, float *out,
+                                  const int32_t *page_table, int32_t max_pages,
+                                  const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                                  int32_t max_seq_len, float scale, void *workspace,
+                                  size_t ws_bytes, void *stream) {
+    return decode_entry(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
+                        workspace, ws_bytes, stream, 2);
 }
 
 SFA_API int sfa_attn_prefill(const sfa_kv_desc *kv, const float *q, float *out,

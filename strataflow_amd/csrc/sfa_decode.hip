@@ -15,10 +15,12 @@
 //     layout of S^T is exactly the B layout P^T needs),
 //   - stages the V tile through LDS (coalesced 16-byte loads in, transposed
 //     2-byte gathers out) to build the V^T operand.
-// Waves merge through LDS; splits merge in the same launch: each workgroup
-// stores (m, l, o) to the workspace and the last one to arrive for a
-// (sequence, kv head) merges all splits in split order, so the result does not
-// depend on arrival order or page placement.
+// Waves merge through LDS; each workgroup stores its (m, l, o) to the
+// workspace and a second kernel merges the splits of each (sequence, head) in
+// split order, so the result does not depend on scheduling or page placement.
+// The kernel boundary is what makes the partials of all eight XCDs visible to
+// the merge (no device-scope fences inside a kernel: on this part each one
+// writes back a whole XCD L2).
 #include "sfa_common.h"
 
 namespace sfa {
@@ -45,10 +47,12 @@ struct DecodeParams {
     int tiles_per_split;  // minimum tiles per split (host heuristic)
     float scale_log2;     // scale * log2(e)
     float *part;          // [B][Hkv][n_splits][G][HD + 4]
-    uint32_t *counters;   // [B][Hkv]
 };
 
 constexpr int kDecodeWaves = 4;
+// merge kernel block: one thread per dim, at least one full wave
+template <int HD>
+constexpr int kMergeThreads = HD < 64 ? 64 : HD;
 
 // Active tile range of sequence b: tiles are 32-aligned absolute position
 // blocks [32t, 32t+32) intersecting [lo, n_kv).
@@ -86,8 +90,6 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
     __shared__ float lds_m[kDecodeWaves][G];
     __shared__ float lds_l[kDecodeWaves][G];
     __shared__ float lds_o[kDecodeWaves][G][HD];
-    __shared__ float lds_w[256];
-    __shared__ int lds_last;
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -137,10 +139,11 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
     const int32_t *pt = p.page_table + (int64_t)b * p.max_pages;
     uint8_t *vt = lds_v[wave];
 
-    for (int t = tile_lo + wave; t < tile_hi; t += kDecodeWaves) {
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    for (int t = tile_lo + wave_u; t < tile_hi; t += kDecodeWaves) {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
-        const int32_t pid = pt[lpage];
+        const int32_t pid = __builtin_amdgcn_readfirstlane(pt[lpage]);
         const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
         const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
         if (kb == nullptr || vb == nullptr) continue;  // invalid page: tile contributes nothing
@@ -276,42 +279,65 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
             }
         }
     }
-    if (n_active == 1) return;
+}
 
-    // last arriver merges the splits
-    __threadfence();
+// Second pass: out = sum_s o_s * 2^(m_s - M) / sum_s l_s * 2^(m_s - M) over
+// the active splits of each (sequence, kv head), in split order.  One
+// workgroup per (b, kv head, group head), one thread per dim.
+template <int HD, int G>
+__global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeParams p) {
+    constexpr int NT = kMergeThreads<HD>;
+    constexpr int NW = NT / kWave;
+    __shared__ float lds_wt[256];
+    __shared__ float lds_red[NW];
+    const int g = blockIdx.x % G;
+    const int kvh = (blockIdx.x / G) % p.n_head_kv;
+    const int b = blockIdx.x / (G * p.n_head_kv);
+    int lo, n_kv, t0, n_tiles, tps, n_active;
+    seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
+    if (n_active <= 1) return;  // written by the split kernel
+    const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
+    const float *pbase = p.part + head_base * p.n_splits * G * (HD + 4) + g * (HD + 4);
+    const int64_t sstride = (int64_t)G * (HD + 4);
+    const int tid = threadIdx.x;
+    // split maxima -> M
+    float M = -INFINITY;
+    for (int s = tid; s < n_active; s += NT) M = fmaxf(M, pbase[s * sstride + HD]);
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    if ((tid & 63) == 0) lds_red[tid >> 6] = M;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&p.counters[head_base], 1u);
-        lds_last = (prev == (uint32_t)(n_active - 1)) ? 1 : 0;
-    }
+    M = lds_red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, lds_red[w]);
     __syncthreads();
-    if (!lds_last) return;
-    __threadfence();
-    const float *pbase = p.part + head_base * p.n_splits * G * (HD + 4);
-    for (int g = 0; g < G; ++g) {
-        float M = -INFINITY;
-        for (int s = threadIdx.x; s < n_active; s += blockDim.x)
-            M = fmaxf(M, pbase[((int64_t)s * G + g) * (HD + 4) + HD]);
-        // block max
-        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        if (lane == 0) lds_w[wave] = M;
-        __syncthreads();
-        M = fmaxf(fmaxf(lds_w[0], lds_w[1]), fmaxf(lds_w[2], lds_w[3]));
-        __syncthreads();
-        for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-            float L = 0.0f, O = 0.0f;
-            for (int s = 0; s < n_active; ++s) {
-                const float *ps = pbase + ((int64_t)s * G + g) * (HD + 4);
-                const float wt = ps[HD] == -INFINITY ? 0.0f : exp2f(ps[HD] - M);
-                L += ps[HD + 1] * wt;
-                O += ps[d] * wt;
-            }
-            out_b[g * HD + d] = L > 0.0f ? O / L : 0.0f;
-        }
-        __syncthreads();
+    // weights and L
+    float L = 0.0f;
+    for (int s = tid; s < n_active; s += NT) {
+        const float m = pbase[s * sstride + HD];
+        const float wt = m == -INFINITY ? 0.0f : exp2f(m - M);
+        lds_wt[s] = wt;
+        L += wt * pbase[s * sstride + HD + 1];
     }
-    if (threadIdx.x == 0) p.counters[head_base] = 0u;
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+    if ((tid & 63) == 0) lds_red[tid >> 6] = L;
+    __syncthreads();
+    L = lds_red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) L += lds_red[w];
+    if (tid >= HD) return;
+    // weighted sum of the split outputs, loads issued in groups of 8
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 8 <= n_active; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = pbase[(s + u) * sstride + tid];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u] * lds_wt[s + u];
+    }
+    for (; s < n_active; ++s) acc += pbase[s * sstride + tid] * lds_wt[s];
+    float *out = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD;
+    out[tid] = L > 0.0f ? acc / L : 0.0f;
 }
 
 // ---- host side -------------------------------------------------------------
@@ -337,24 +363,28 @@ SplitPlan plan_splits(int B, int Hkv, int max_seq_len) {
 
 size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
     const SplitPlan sp = plan_splits(B, Hkv, max_seq_len);
-    const size_t counters = ((size_t)B * Hkv * sizeof(uint32_t) + 255) & ~(size_t)255;
-    const size_t part = (size_t)B * Hkv * sp.n_splits * G * (HD + 4) * sizeof(float);
-    return counters + part;
+    return (size_t)B * Hkv * sp.n_splits * G * (HD + 4) * sizeof(float);
 }
 
+// pass bit 1: split-K pass, bit 2: merge pass
 template <int HD, int G>
-static void launch_f16(const DecodeParams &p, int B, int Hkv, hipStream_t s) {
-    dim3 grid(p.n_splits, Hkv, B);
-    hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
+static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStream_t s) {
+    if (passes & 1) {
+        dim3 grid(p.n_splits, Hkv, B);
+        hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
+    }
+    if ((passes & 2) && p.n_splits > 1)
+        hipLaunchKernelGGL((decode_merge_kernel<HD, G>), dim3(B * Hkv * G), dim3(kMergeThreads<HD>), 0,
+                           s, p);
 }
 
 template <int HD>
-static int launch_f16_g(const DecodeParams &p, int G, int B, int Hkv, hipStream_t s) {
+static int launch_f16_g(const DecodeParams &p, int G, int B, int Hkv, int passes, hipStream_t s) {
     switch (G) {
-    case 1: launch_f16<HD, 1>(p, B, Hkv, s); return SFA_OK;
-    case 2: launch_f16<HD, 2>(p, B, Hkv, s); return SFA_OK;
-    case 4: launch_f16<HD, 4>(p, B, Hkv, s); return SFA_OK;
-    case 8: launch_f16<HD, 8>(p, B, Hkv, s); return SFA_OK;
+    case 1: launch_f16<HD, 1>(p, B, Hkv, passes, s); return SFA_OK;
+    case 2: launch_f16<HD, 2>(p, B, Hkv, passes, s); return SFA_OK;
+    case 4: launch_f16<HD, 4>(p, B, Hkv, passes, s); return SFA_OK;
+    case 8: launch_f16<HD, 8>(p, B, Hkv, passes, s); return SFA_OK;
     default: return SFA_ERR_UNSUPPORTED;
     }
 }
@@ -362,7 +392,7 @@ static int launch_f16_g(const DecodeParams &p, int G, int B, int Hkv, hipStream_
 int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
                   int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
                   int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
-                  hipStream_t stream) {
+                  int passes, hipStream_t stream) {
     const int Hkv = kv->n_head_kv, HD = kv->head_dim, G = kv->n_head / kv->n_head_kv;
     if (B <= 0 || max_seq_len <= 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
     if (q == nullptr || out == nullptr || page_table == nullptr || seq_len == nullptr)
@@ -370,7 +400,6 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     const size_t need = decode_workspace_bytes(B, Hkv, G, HD, max_seq_len);
     if (workspace == nullptr || ws_bytes < need) return SFA_ERR_INVALID_ARGUMENT;
     const SplitPlan sp = plan_splits(B, Hkv, max_seq_len);
-    const size_t counters = ((size_t)B * Hkv * sizeof(uint32_t) + 255) & ~(size_t)255;
 
     DecodeParams p;
     p.k_pages = static_cast<const uint8_t *>(kv->k_pages);
@@ -393,15 +422,14 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     p.n_splits = sp.n_splits;
     p.tiles_per_split = sp.tiles_per_split;
     p.scale_log2 = scale * 1.4426950408889634f;
-    p.counters = static_cast<uint32_t *>(workspace);
-    p.part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + counters);
+    p.part = static_cast<float *>(workspace);
 
     if (kv->kv_type != SFA_KV_F16) return SFA_ERR_UNSUPPORTED;
     int rc;
     switch (HD) {
-    case 32: rc = launch_f16_g<32>(p, G, B, Hkv, stream); break;
-    case 64: rc = launch_f16_g<64>(p, G, B, Hkv, stream); break;
-    case 128: rc = launch_f16_g<128>(p, G, B, Hkv, stream); break;
+    case 32: rc = launch_f16_g<32>(p, G, B, Hkv, passes, stream); break;
+    case 64: rc = launch_f16_g<64>(p, G, B, Hkv, passes, stream); break;
+    case 128: rc = launch_f16_g<128>(p, G, B, Hkv, passes, stream); break;
     default: return SFA_ERR_UNSUPPORTED;
     }
     if (rc != SFA_OK) return rc;

@@ -59,11 +59,16 @@ class PagedKV:
         else:
             self.k_cold = self.v_cold = None
         self._ws = None
-        self._ws_key = None
+        self._ws_need = {}
+        self._descs = [self._make_desc(layer) for layer in range(n_layer)]
         lib = _lib.load()
         _lib.check(lib.sfa_kv_desc_check(ctypes.byref(self.desc(0))), "kv descriptor")
 
     def desc(self, layer: int) -> SfaKvDesc:
+        """The sfa_kv_desc of one layer (built once; pool pointers are stable)."""
+        return self._descs[layer]
+
+    def _make_desc(self, layer: int) -> SfaKvDesc:
         d = SfaKvDesc()
         d.n_head, d.n_head_kv, d.head_dim = self.n_head, self.n_head_kv, self.head_dim
         d.page_size, d.kv_type, d.n_pages = self.page_size, self.kv_type, self.n_pages
@@ -82,9 +87,12 @@ class PagedKV:
     # -- workspace -------------------------------------------------------------
     def workspace(self, B: int, max_seq_len: int) -> torch.Tensor:
         lib = _lib.load()
-        need = lib.sfa_decode_workspace_bytes(ctypes.byref(self.desc(0)), B, max_seq_len)
-        if need == 0:
-            raise ValueError("invalid decode shape")
+        need = self._ws_need.get((B, max_seq_len))
+        if need is None:
+            need = lib.sfa_decode_workspace_bytes(ctypes.byref(self.desc(0)), B, max_seq_len)
+            if need == 0:
+                raise ValueError("invalid decode shape")
+            self._ws_need[(B, max_seq_len)] = need
         if self._ws is None or self._ws.numel() < need:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
             _lib.check(lib.sfa_workspace_init(self._ws.data_ptr(), self._ws.numel(), _stream(None)),
@@ -106,8 +114,10 @@ class PagedKV:
 
     def decode(self, layer: int, q: torch.Tensor, page_table: torch.Tensor, seq_len: torch.Tensor,
                max_seq_len: int, kv_lo: torch.Tensor | None = None, out: torch.Tensor | None = None,
-               scale: float | None = None, stream=None) -> torch.Tensor:
-        """q [B, Hq, hd] f32 -> out [B, Hq*hd] f32."""
+               scale: float | None = None, stream=None, split_end_event=None) -> torch.Tensor:
+        """q [B, Hq, hd] f32 -> out [B, Hq*hd] f32.  With `split_end_event` the
+        two passes are issued separately and the event is recorded between
+        them (timing of the split-K pass)."""
         B = int(seq_len.numel())
         assert q.is_contiguous() and q.dtype == torch.float32
         assert q.shape == (B, self.n_head, self.head_dim)
@@ -116,13 +126,17 @@ class PagedKV:
             out = torch.empty((B, self.n_head * self.head_dim), dtype=torch.float32, device=q.device)
         ws = self.workspace(B, max_seq_len)
         lib = _lib.load()
-        d = self.desc(layer)
-        _lib.check(lib.sfa_attn_decode(ctypes.byref(d), q.data_ptr(), out.data_ptr(),
-                                       page_table.data_ptr(), int(page_table.shape[1]),
-                                       seq_len.data_ptr(), _ptr(kv_lo), B, int(max_seq_len),
-                                       float(scale if scale is not None else self.scale),
-                                       ws.data_ptr(), ws.numel(), _stream(stream)),
-                   "sfa_attn_decode")
+        d = self._descs[layer]
+        args = (ctypes.byref(d), q.data_ptr(), out.data_ptr(), page_table.data_ptr(),
+                int(page_table.shape[1]), seq_len.data_ptr(), _ptr(kv_lo), B, int(max_seq_len),
+                float(scale if scale is not None else self.scale), ws.data_ptr(), ws.numel(),
+                _stream(stream))
+        if split_end_event is None:
+            _lib.check(lib.sfa_attn_decode(*args), "sfa_attn_decode")
+        else:
+            _lib.check(lib.sfa_attn_decode_split(*args), "sfa_attn_decode_split")
+            split_end_event.record()
+            _lib.check(lib.sfa_attn_decode_merge(*args), "sfa_attn_decode_merge")
         return out
 
     def prefill(self, layer: int, q: torch.Tensor, page_table: torch.Tensor, q_pos0: int,
