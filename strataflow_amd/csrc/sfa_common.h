@@ -48,6 +48,18 @@ __device__ inline const uint8_t *page_base(int32_t id, const uint8_t *pool, int 
     return nullptr;
 }
 
+// ds_read_b64_tr_b16: with every lane of a 16-lane group addressing an
+// 8-byte chunk of four 16-bit values, lane i of the group receives value i%4
+// of the chunks addressed by lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4 (in that
+// order).  The address must be 8-byte aligned.
+__device__ inline half4 tr16_read(const uint8_t *lds_addr) {
+    typedef short short4_t __attribute__((ext_vector_type(4)));
+    const auto p = (__attribute__((address_space(3))) short4_t *)(
+        (__attribute__((address_space(3))) uint8_t *)(lds_addr));
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p);
+    return __builtin_bit_cast(half4, v);
+}
+
 // Cross-half exchange: value of lane (l ^ 32).
 __device__ inline float xor32(float x) {
     return __shfl_xor(x, 32, 64);

@@ -98,10 +98,48 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
     const int wave = threadIdx.x >> 6;
     const int n = lane & 31;   // MFMA column (head replica) / A-operand row
     const int hh = lane >> 5;  // k half
+    const int32_t *pt = p.page_table + (int64_t)b * p.max_pages;
+
+    const int Hkv = p.n_head_kv;
+    const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
+    uint8_t *vt = lds_v[wave];
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+    // Issues the K (A operand: row n, dims 16c + 8hh) and V (coalesced: row
+    // i*RPI + lane/CPR, chunk lane%CPR) loads of tile t.  The loads do not
+    // depend on seq_len: every row of a tile lies in one existing page, and
+    // rows outside [lo, n_kv) are masked after arrival (score -inf, V zeroed).
+    // Returns false (wave-uniform) when the tile's page id is invalid.
+    half8 kf[KC];
+    half8 vr[VIT];
+    auto issue = [&](int t) -> bool {
+        const int pos0 = t * kTile;
+        const int lpage = pos0 / p.page_size;
+        if (lpage >= p.max_pages) return false;
+        const int32_t pid = __builtin_amdgcn_readfirstlane(pt[lpage]);
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        if (kb == nullptr || vb == nullptr) return false;
+        const int64_t off0 = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
+        const uint8_t *kr = kb + off0 + (int64_t)n * col_bytes + 16 * hh;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) kf[c] = *reinterpret_cast<const half8 *>(kr + 32 * c);
+#pragma unroll
+        for (int i = 0; i < VIT; ++i) {
+            const int r = i * RPI + lane / CPR;
+            vr[i] = *reinterpret_cast<const half8 *>(vb + off0 + (int64_t)r * col_bytes + 16 * (lane % CPR));
+        }
+        return true;
+    };
+
+    // The first tile as the host plan places it (kv_lo 0, seq_len within the
+    // plan) is fetched before seq_len is known; re-issued below if the guess
+    // was wrong.
+    const int t_guess = __builtin_amdgcn_readfirstlane(split * p.tiles_per_split + wave);
+    bool tile_ok = issue(t_guess);
 
     int lo, n_kv, t0, n_tiles, tps, n_active;
     seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
-    const int Hkv = p.n_head_kv;
     float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
     if (split >= n_active) {
         if (split == 0 && n_active == 0) {
@@ -109,9 +147,15 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
         }
         return;
     }
+    const int tile_lo = t0 + split * tps;
+    int tile_hi = tile_lo + tps;
+    if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
+    int t = tile_lo + wave_u;
+    if (t != t_guess) tile_ok = t < tile_hi ? issue(t) : false;
 
     // Q^T operand: column n -> head kvh*G + n%G, dims 16c + 8hh .. +8, f16
-    // (the F16 vec_dot_type conversion ggml applies to src1).
+    // (the F16 vec_dot_type conversion ggml applies to src1).  Loaded after
+    // the first tile's K/V so both latencies overlap.
     half8 qf[KC];
     {
         const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G + (n % G)) * HD;
@@ -132,59 +176,33 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
     float m_run = -INFINITY;
     float l_run = 0.0f;
 
-    const int tile_lo = t0 + split * tps;
-    int tile_hi = tile_lo + tps;
-    if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
-    const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
-    const int32_t *pt = p.page_table + (int64_t)b * p.max_pages;
-    uint8_t *vt = lds_v[wave];
-
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    for (int t = tile_lo + wave_u; t < tile_hi; t += kDecodeWaves) {
+    bool first = true;
+    for (; t < tile_hi; t += kDecodeWaves) {
         const int pos0 = t * kTile;
-        const int lpage = pos0 / p.page_size;
-        const int32_t pid = __builtin_amdgcn_readfirstlane(pt[lpage]);
-        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
-        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
-        if (kb == nullptr || vb == nullptr) continue;  // invalid page: tile contributes nothing
-        const int64_t off0 = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
-
-        // K rows into the A operand: row n, dims 16c + 8hh.
-        const int kpos = pos0 + n;
-        const bool kvalid = kpos >= lo && kpos < n_kv;
-        half8 kf[KC];
-        {
-            const uint8_t *kr = kb + off0 + (int64_t)n * col_bytes + 16 * hh;
-#pragma unroll
-            for (int c = 0; c < KC; ++c) {
-                kf[c] = kvalid ? *reinterpret_cast<const half8 *>(kr + 32 * c) : half8{};
-            }
+        if (!tile_ok) {  // invalid page id: this tile contributes nothing
+            tile_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
+            continue;
         }
-        // V rows, coalesced: row r = i*RPI + lane/CPR, chunk lane%CPR.
-        half8 vr[VIT];
+        // S^T = K * Q^T, two accumulation chains
+        floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+        for (int c = 0; c < KC; c += 2) {
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s0, 0, 0, 0);
+            if (c + 1 < KC) s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c + 1], qf[c + 1], s1, 0, 0, 0);
+        }
+        // V tile into the wave's LDS region; rows outside [lo, n_kv) zeroed
+        // (they may hold stale bytes of a page's unused tail)
 #pragma unroll
         for (int i = 0; i < VIT; ++i) {
             const int r = i * RPI + lane / CPR;
-            const int vpos = pos0 + r;
-            const bool vvalid = vpos >= lo && vpos < n_kv;
-            const uint8_t *src = vb + off0 + (int64_t)r * col_bytes + 16 * (lane % CPR);
-            vr[i] = vvalid ? *reinterpret_cast<const half8 *>(src) : half8{};
+            const bool ok = pos0 + r >= lo && pos0 + r < n_kv;
+            *reinterpret_cast<half8 *>(vt + r * VROW + 16 * (lane % CPR)) = ok ? vr[i] : half8{};
         }
+        // registers are free: start the next tile's loads now
+        const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
 
-        // S^T = K * Q^T
-        floatx16 s = floatx16{};
-#pragma unroll
-        for (int c = 0; c < KC; ++c) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s, 0, 0, 0);
-
-        // V tile into LDS (wave-private region) while the MFMAs drain.
-#pragma unroll
-        for (int i = 0; i < VIT; ++i) {
-            const int r = i * RPI + lane / CPR;
-            *reinterpret_cast<half8 *>(vt + r * VROW + 16 * (lane % CPR)) = vr[i];
-        }
-
-        // online softmax (log2 domain); row of register i is position
-        // 8(i/4) + 4hh + i%4 of the tile.
+        // online softmax (log2 domain); row of register i is tile position
+        // 8(i/4) + 4hh + i%4
         float sv[16];
         float mt = -INFINITY;
 #pragma unroll
@@ -192,47 +210,69 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
             const int r = 8 * (i >> 2) + 4 * hh + (i & 3);
             const int pp = pos0 + r;
             const bool ok = pp >= lo && pp < n_kv;
-            sv[i] = ok ? s[i] * p.scale_log2 : -INFINITY;
+            sv[i] = ok ? (s0[i] + s1[i]) * p.scale_log2 : -INFINITY;
             mt = fmaxf(mt, sv[i]);
         }
         mt = fmaxf(mt, xor32(mt));
         const float m_new = fmaxf(m_run, mt);
-        const float alpha = exp2f(m_run - m_new);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = exp2f(m_run - m_use);
         float ls = 0.0f;
         half8 pb[2];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float e = exp2f(sv[i] - m_new);
+            const float e = exp2f(sv[i] - m_use);
             ls += e;
             pb[i >> 3][i & 7] = (_Float16)e;
         }
         l_run = l_run * alpha + ls;
         m_run = m_new;
+        if (!first) {  // o is still zero on the first tile
 #pragma unroll
-        for (int d = 0; d < DB; ++d) o[d] *= alpha;
+            for (int d = 0; d < DB; ++d) o[d] *= alpha;
+        }
+        first = false;
 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        // O^T += V^T * P^T; k index 8hh + j of chunk kk is tile position
+        // V^T operands: k index 8hh + j of chunk kk is tile position
         // 16kk + 8(j/4) + 4hh + j%4 (the rows this lane holds in pb[kk]).
+        // ds_read_b64_tr_b16 hands lane i of each 16-lane group column i%4 of
+        // the 8-byte chunks addressed by lanes i/4 + 4j (j = 0..3), so lane
+        // r of group gq supplies chunk (position 16kk + 8u + 4(gq/2) + r/4,
+        // dims 32d + 16(gq%2) + 4(r%4)) and receives its own dim n at the four
+        // positions of half u.
+        half8 va[2][DB];
+        {
+            const int gq = lane >> 4, rr = lane & 15;
+            const uint8_t *vsrc = vt + (4 * (gq >> 1) + (rr >> 2)) * VROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const half4 h = tr16_read(vsrc + (16 * kk + 8 * u) * VROW + 64 * d);
+                        va[kk][d][4 * u + 0] = h[0];
+                        va[kk][d][4 * u + 1] = h[1];
+                        va[kk][d][4 * u + 2] = h[2];
+                        va[kk][d][4 * u + 3] = h[3];
+                    }
+                }
+            }
+        }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-            for (int d = 0; d < DB; ++d) {
-                half8 a;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int r = 16 * kk + 8 * (j >> 2) + 4 * hh + (j & 3);
-                    a[j] = *reinterpret_cast<const _Float16 *>(vt + r * VROW + 2 * (32 * d + n));
-                }
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kk], o[d], 0, 0, 0);
-            }
+            for (int d = 0; d < DB; ++d)
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kk][d], pb[kk], o[d], 0, 0, 0);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        tile_ok = next_ok;
     }
 
     // wave partial -> LDS (column n < G is head n; dims of register i of block
@@ -286,58 +326,48 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
 // workgroup per (b, kv head, group head), one thread per dim.
 template <int HD, int G>
 __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeParams p) {
-    constexpr int NT = kMergeThreads<HD>;
-    constexpr int NW = NT / kWave;
-    __shared__ float lds_wt[256];
-    __shared__ float lds_red[NW];
+    constexpr int CH = 32;  // splits whose loads are in flight together
     const int g = blockIdx.x % G;
     const int kvh = (blockIdx.x / G) % p.n_head_kv;
     const int b = blockIdx.x / (G * p.n_head_kv);
+    const int tid = threadIdx.x;
     int lo, n_kv, t0, n_tiles, tps, n_active;
     seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
-    if (n_active <= 1) return;  // written by the split kernel
+    if (n_active <= 1 || tid >= HD) return;  // one split: written by the split pass
     const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
     const float *pbase = p.part + head_base * p.n_splits * G * (HD + 4) + g * (HD + 4);
     const int64_t sstride = (int64_t)G * (HD + 4);
-    const int tid = threadIdx.x;
-    // split maxima -> M
-    float M = -INFINITY;
-    for (int s = tid; s < n_active; s += NT) M = fmaxf(M, pbase[s * sstride + HD]);
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    if ((tid & 63) == 0) lds_red[tid >> 6] = M;
-    __syncthreads();
-    M = lds_red[0];
+    // log-sum-exp merge in split order, CH splits per round: every load of a
+    // round is issued before any is used
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int s0 = 0; s0 < n_active; s0 += CH) {
+        float m[CH], l[CH], o[CH];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) M = fmaxf(M, lds_red[w]);
-    __syncthreads();
-    // weights and L
-    float L = 0.0f;
-    for (int s = tid; s < n_active; s += NT) {
-        const float m = pbase[s * sstride + HD];
-        const float wt = m == -INFINITY ? 0.0f : exp2f(m - M);
-        lds_wt[s] = wt;
-        L += wt * pbase[s * sstride + HD + 1];
+        for (int u = 0; u < CH; ++u) {
+            const int s = s0 + u < n_active ? s0 + u : n_active - 1;
+            const float *ps = pbase + s * sstride;
+            m[u] = ps[HD];
+            l[u] = ps[HD + 1];
+            o[u] = ps[tid];
+        }
+        float mc = M;
+#pragma unroll
+        for (int u = 0; u < CH; ++u)
+            if (s0 + u < n_active) mc = fmaxf(mc, m[u]);
+        if (mc == -INFINITY) continue;
+        const float a = exp2f(M - mc);  // M == -inf -> 0
+        L *= a;
+        O *= a;
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const float w = (s0 + u < n_active && m[u] != -INFINITY) ? exp2f(m[u] - mc) : 0.0f;
+            L += l[u] * w;
+            O += o[u] * w;
+        }
+        M = mc;
     }
-    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
-    if ((tid & 63) == 0) lds_red[tid >> 6] = L;
-    __syncthreads();
-    L = lds_red[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) L += lds_red[w];
-    if (tid >= HD) return;
-    // weighted sum of the split outputs, loads issued in groups of 8
-    float acc = 0.0f;
-    int s = 0;
-    for (; s + 8 <= n_active; s += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = pbase[(s + u) * sstride + tid];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc += v[u] * lds_wt[s + u];
-    }
-    for (; s < n_active; ++s) acc += pbase[s * sstride + tid] * lds_wt[s];
     float *out = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD;
-    out[tid] = L > 0.0f ? acc / L : 0.0f;
+    out[tid] = L > 0.0f ? O / L : 0.0f;
 }
 
 // ---- host side -------------------------------------------------------------
@@ -348,7 +378,7 @@ struct SplitPlan {
 };
 
 SplitPlan plan_splits(int B, int Hkv, int max_seq_len) {
-    const int tiles = (max_seq_len + kTile - 1) / kTile + 1;
+    const int tiles = (max_seq_len + kTile - 1) / kTile;
     const int heads = B * Hkv;
     const int wg_target = 1024;
     int S = (wg_target + heads - 1) / heads;
