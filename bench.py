@@ -35,29 +35,37 @@ MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense f16/bf16
 N_LAYER, HQ, HKV, HD, PAGE = 32, 32, 8, 128, 256
 
 
-def build_decode_workload(torch, ctx: int, seed: int):
+def build_decode_workload(torch, ctx, seed: int, kv_type: int = 1):
+    """N_LAYER distinct paged caches holding sequences of lengths `ctx` (an int
+    or a list, one entry per sequence), pages of all sequences drawn from one
+    shuffled pool per layer; K/V ~ N(0,1) with RoPE theta 1e6 on K, written
+    through sfa_kv_append (f16 rounding or Q8_0 quantisation on write)."""
     from strataflow_amd import synth
-    from strataflow_amd.paged_kv import PagedKV, SFA_KV_F16
+    from strataflow_amd.paged_kv import PagedKV
     dev = torch.device("cuda:0")
-    n_pages = (ctx + PAGE - 1) // PAGE
-    pool_pages = n_pages + 4
-    kv = PagedKV(N_LAYER, HQ, HKV, HD, SFA_KV_F16, PAGE, pool_pages, device=dev)
+    lens = [ctx] if isinstance(ctx, int) else [int(x) for x in ctx]
+    B = len(lens)
+    need = sum((n + PAGE - 1) // PAGE for n in lens)
+    pool_pages = need + 4
+    kv = PagedKV(N_LAYER, HQ, HKV, HD, kv_type, PAGE, pool_pages, device=dev)
     rng = np.random.default_rng(seed)
-    pt = synth.page_tables(rng, [ctx], PAGE, pool_pages)
+    pt = synth.page_tables(rng, lens, PAGE, pool_pages)
     t_pt = torch.from_numpy(pt).to(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    pos = torch.arange(ctx, device=dev, dtype=torch.int32)
-    seq = torch.zeros(ctx, device=dev, dtype=torch.int32)
     for layer in range(N_LAYER):
-        k = torch.randn((ctx, HKV, HD), device=dev, generator=gen)
-        v = torch.randn((ctx, HKV, HD), device=dev, generator=gen)
-        k = synth.rope_normal_torch(k, pos, 1e6).contiguous()
-        kv.append(layer, k, v, seq, pos, t_pt)
-    q = torch.randn((N_LAYER, 1, HQ, HD), device=dev, generator=gen)
-    qpos = torch.full((1,), ctx - 1, device=dev, dtype=torch.int32)
+        for b, n in enumerate(lens):
+            pos = torch.arange(n, device=dev, dtype=torch.int32)
+            seq = torch.full((n,), b, device=dev, dtype=torch.int32)
+            k = torch.randn((n, HKV, HD), device=dev, generator=gen)
+            v = torch.randn((n, HKV, HD), device=dev, generator=gen)
+            k = synth.rope_normal_torch(k, pos, 1e6).contiguous()
+            kv.append(layer, k, v, seq, pos, t_pt)
+            del k, v
+    q = torch.randn((N_LAYER, B, HQ, HD), device=dev, generator=gen)
+    qpos = torch.tensor([n - 1 for n in lens], device=dev, dtype=torch.int32)
     q = torch.stack([synth.rope_normal_torch(q[i], qpos, 1e6) for i in range(N_LAYER)]).contiguous()
-    seq_len = torch.tensor([ctx], device=dev, dtype=torch.int32)
+    seq_len = torch.tensor(lens, device=dev, dtype=torch.int32)
     torch.cuda.synchronize()
     return kv, pt, t_pt, q, seq_len
 
@@ -86,8 +94,9 @@ def time_decode(torch, kv, t_pt, q, seq_len, ctx, steps, warmup):
     replayed `steps` times between two events.  Kernel timing: events around
     every split-K launch of the same loop, queued behind a backlog so the
     launches run back to back."""
-    out = torch.empty((N_LAYER, 1, HQ * HD), device=q.device)
-    kv.workspace(1, ctx)
+    B = int(seq_len.numel())
+    out = torch.empty((N_LAYER, B, HQ * HD), device=q.device)
+    kv.workspace(B, ctx)
 
     def step():
         for layer in range(N_LAYER):
@@ -132,6 +141,37 @@ def time_decode(torch, kv, t_pt, q, seq_len, ctx, steps, warmup):
     torch.cuda.synchronize()
     durs = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3  # us
     return ms_per_step, ms_eager, float(np.mean(durs)), float(np.median(durs)), out
+
+
+def q8_bench(torch, steps, warmup, seed):
+    """Q8_0 KV decode: (a) batch 1 at context 32768; (b) batch 8 with lengths
+    uniform in [8192, 32768] sharing one page pool."""
+    res = {}
+    row_q8 = HD // 32 * 34
+    for name, lens in (("ctx32k_b1", [32768]),
+                       ("b8_varlen_8k_32k", [int(x) for x in np.random.default_rng(seed).integers(8192, 32769, 8)])):
+        kv, pt, t_pt, q, seq_len = build_decode_workload(torch, lens, seed, kv_type=8)
+        mx = int(max(lens))
+        ms, ms_eager, k_mean, k_med, _ = time_decode(torch, kv, t_pt, q, seq_len, mx, steps, warmup)
+        kv_bytes = 2 * sum(lens) * HKV * row_q8
+        alg = kv_bytes + len(lens) * HQ * HD * 4 * 2
+        us_layer = ms * 1e3 / N_LAYER
+        ach = alg / (k_mean * 1e-6) / 1e9
+        res[name] = {
+            "workload": f"decode-attn Q8_0 KV, Mixtral GQA 32q/8kv hd128, B={len(lens)}, "
+                        f"context {lens if len(lens) > 1 else lens[0]}, 256-token pages shuffled, "
+                        f"{N_LAYER} layers",
+            "us_per_layer_step": round(us_layer, 3),
+            "us_per_layer_token": round(us_layer / len(lens), 3),
+            "tokens_per_s": round(len(lens) * 1e3 / ms, 1),
+            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "decode_q8_kernel<128,4> (split-K pass)",
+                         "kernel_us_mean": round(k_mean, 3), "bytes_per_launch": alg},
+        }
+        del kv, q
+        torch.cuda.empty_cache()
+    return res
 
 
 def prefill_bench(torch, steps: int, warmup: int, seed: int):
@@ -227,6 +267,7 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 decode legs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
     args = ap.parse_args()
@@ -293,6 +334,8 @@ def main():
     }
     if not args.no_prefill:
         result["prefill"] = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1)
+    if not args.no_q8:
+        result["q8_0"] = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2)
     if not args.no_cpu:
         threads, res = cpu_baseline(kv, pt, q[0], ctx)
         us_all, n_all, cpu_out = res[threads]

@@ -60,6 +60,17 @@ __device__ inline half4 tr16_read(const uint8_t *lds_addr) {
     return __builtin_bit_cast(half4, v);
 }
 
+// 16- and 4-byte global loads from 4-byte aligned addresses (Q8_0 rows are
+// only 4-byte aligned; global loads need dword alignment on this target).
+__device__ inline intx4 load16_a4(const uint8_t *p) {
+    intx4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 4), 16);
+    return v;
+}
+__device__ inline uint32_t load4_a4(const uint8_t *p) {
+    return *reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
+}
+
 // Cross-half exchange: value of lane (l ^ 32).
 __device__ inline float xor32(float x) {
     return __shfl_xor(x, 32, 64);

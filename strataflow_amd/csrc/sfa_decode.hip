@@ -37,6 +37,7 @@ struct DecodeParams {
     int n_head_kv;
     int n_head;
     int row_bytes;
+    int kv_type;
     const float *q;
     float *out;
     const int32_t *page_table;
@@ -73,6 +74,58 @@ __device__ inline void seq_tiles(const DecodeParams &p, int b, int &lo, int &n_k
     const int need = (n_tiles + p.n_splits - 1) / p.n_splits;
     if (tps < need) tps = need;
     n_active = (n_tiles + tps - 1) / tps;
+}
+
+// Workgroup epilogue of a split: the four waves' (m, l, O^T) for the g heads
+// (MFMA column n < g is head n; register i of dim block d holds dim
+// 32d + 8(i/4) + 4hh + i%4) merge through LDS into the split's (m, l, o),
+// written to the workspace, or straight to the output when the sequence has
+// one split.  `l_run` is the lane's full sum over its tiles.
+template <int HD, int G>
+__device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run, float l_run,
+                                      float (*lds_m)[G], float (*lds_l)[G], float (*lds_o)[G][HD],
+                                      const DecodeParams &p, int b, int kvh, int split, int n_active,
+                                      float *out_b, int wave, int n, int hh) {
+    constexpr int DB = HD / 32;
+    if (n < G) {
+        if (hh == 0) {
+            lds_m[wave][n] = m_run;
+            lds_l[wave][n] = l_run;
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                lds_o[wave][n][32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i];
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
+    float *part = p.part + (head_base * p.n_splits + split) * G * (HD + 4);
+    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
+        const int g = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, lds_m[w][g]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            const float mw = lds_m[w][g];
+            const float wt = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+            L += lds_l[w][g] * wt;
+            O += lds_o[w][g][d] * wt;
+        }
+        if (n_active == 1) {
+            out_b[g * HD + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            part[g * (HD + 4) + d] = O;
+            if (d == 0) {
+                part[g * (HD + 4) + HD] = M;
+                part[g * (HD + 4) + HD + 1] = L;
+            }
+        }
+    }
 }
 
 template <int HD, int G>
@@ -275,50 +328,319 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
         tile_ok = next_ok;
     }
 
-    // wave partial -> LDS (column n < G is head n; dims of register i of block
-    // d are 32d + 8(i/4) + 4hh + i%4)
     l_run += xor32(l_run);
-    if (n < G) {
-        if (hh == 0) {
-            lds_m[wave][n] = m_run;
-            lds_l[wave][n] = l_run;
-        }
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                lds_o[wave][n][32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i];
-            }
-        }
-    }
-    __syncthreads();
+    split_epilogue<HD, G>(o, m_run, l_run, lds_m, lds_l, lds_o, p, b, kvh, split, n_active, out_b,
+                          wave, n, hh);
+}
 
-    // merge the waves; the workgroup's (m, l, o) per head
-    const int64_t head_base = (int64_t)b * Hkv + kvh;
-    float *part = p.part + (head_base * p.n_splits + split) * G * (HD + 4);
-    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
-        const int g = idx / HD, d = idx % HD;
-        float M = -INFINITY;
+// Q8_0 decode (head_dim 64 or 128).  A row is head_dim/32 ggml block_q8_0
+// records {fp16 d; int8 q[32]} of 34 bytes; rows start 4-byte aligned (the
+// row is 68 or 136 bytes), so block c starts at 2c mod 4 and every byte
+// offset below is a compile-time constant modulo 4.
+//   - Q is quantised to Q8_0 in the prologue exactly as ggml's mul_mat does
+//     for a Q8_0 src0 (vec_dot_type Q8_0: d = amax/127 stored fp16,
+//     q = round(x/d)), and S = Q * K^T runs on v_mfma_i32_32x32x32_i8, one
+//     MFMA per block, then s += float(sumi) * (d_k * d_q) per block in block
+//     order: ggml_vec_dot_q8_0_q8_0's arithmetic.  Rows of the MFMA are the
+//     query heads (row m is head m % g), columns are the 32 tile positions,
+//     so each lane owns one position and its d_k.
+//   - V is dequantised in registers (q * d, rounded to f16) into the same
+//     LDS tile layout as the f16 path, and P goes through LDS to the P^T
+//     operand; PV is the f16 path's O^T = V^T * P^T.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void decode_q8_kernel(DecodeParams p) {
+    static_assert(HD == 64 || HD == 128, "head_dim");
+    static_assert(G >= 1 && G <= 8 && (8 % G) == 0, "group size");
+    constexpr int NB = HD / 32;          // blocks per row
+    constexpr int DB = HD / 32;          // 32-dim blocks of the PV output
+    constexpr int VROW = HD * 2 + 16;    // padded LDS row of the f16 V tile
+    constexpr int VBL = NB / 2;          // V blocks dequantised per lane
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[kDecodeWaves][kTile * VROW];
+    __shared__ __attribute__((aligned(16))) _Float16 lds_p[kDecodeWaves][G][kTile];
+    __shared__ float lds_dq[G][NB];
+    __shared__ float lds_m[kDecodeWaves][G];
+    __shared__ float lds_l[kDecodeWaves][G];
+    __shared__ float lds_o[kDecodeWaves][G][HD];
+
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 31;   // tile position (QK) / MFMA column (PV)
+    const int hh = lane >> 5;
+    const int32_t *pt = p.page_table + (int64_t)b * p.max_pages;
+    const int Hkv = p.n_head_kv;
+    const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
+    uint8_t *vt = lds_v[wave];
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+    // K operand of block c for lane (row n, half hh): quants 16hh..16hh+15 of
+    // block c and the block scale; V: blocks VBL*hh .. of row n, raw.
+    intx4 kq[NB];
+    uint32_t kd[NB];             // dword holding d_k of block c
+    uint32_t vw[VBL][9];         // the 36 bytes around each V block
+    auto issue = [&](int t) -> bool {
+        const int pos0 = t * kTile;
+        const int lpage = pos0 / p.page_size;
+        if (lpage >= p.max_pages) return false;
+        const int32_t pid = __builtin_amdgcn_readfirstlane(pt[lpage]);
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        if (kb == nullptr || vb == nullptr) return false;
+        const int64_t off = (int64_t)(pos0 - lpage * p.page_size + n) * col_bytes + (int64_t)kvh * p.row_bytes;
+        const uint8_t *kr = kb + off;
+        const uint8_t *vr = vb + off;
 #pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, lds_m[w][g]);
-        float L = 0.0f, O = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
-            const float mw = lds_m[w][g];
-            const float wt = mw == -INFINITY ? 0.0f : exp2f(mw - M);
-            L += lds_l[w][g] * wt;
-            O += lds_o[w][g][d] * wt;
-        }
-        if (n_active == 1) {
-            out_b[g * HD + d] = L > 0.0f ? O / L : 0.0f;
-        } else {
-            part[g * (HD + 4) + d] = O;
-            if (d == 0) {
-                part[g * (HD + 4) + HD] = M;
-                part[g * (HD + 4) + HD + 1] = L;
+        for (int c = 0; c < NB; ++c) {
+            if ((c & 1) == 0) {
+                // block at 34c (4-aligned): quants of half hh start 2 bytes
+                // into the dword at 34c + 16hh; d is the low half at 34c
+                const uint8_t *w = kr + 34 * c + 16 * hh;
+                const intx4 x = load16_a4(w);
+                const uint32_t x4 = load4_a4(w + 16);
+                kq[c][0] = (int)__builtin_amdgcn_alignbyte((uint32_t)x[1], (uint32_t)x[0], 2);
+                kq[c][1] = (int)__builtin_amdgcn_alignbyte((uint32_t)x[2], (uint32_t)x[1], 2);
+                kq[c][2] = (int)__builtin_amdgcn_alignbyte((uint32_t)x[3], (uint32_t)x[2], 2);
+                kq[c][3] = (int)__builtin_amdgcn_alignbyte(x4, (uint32_t)x[3], 2);
+                kd[c] = load4_a4(kr + 34 * c);
+            } else {
+                // block at 34c (2 mod 4): quants 4-aligned; d is the high half
+                // of the dword at 34c - 2
+                kq[c] = load16_a4(kr + 34 * c + 2 + 16 * hh);
+                kd[c] = load4_a4(kr + 34 * c - 2);
             }
         }
+#pragma unroll
+        for (int u = 0; u < VBL; ++u) {
+            const int c = VBL * hh + u;
+            // 9 dwords from the 4-aligned address at or 2 bytes below the block
+            const uint8_t *w = vr + 34 * c - (c & 1) * 2;
+            const intx4 a0 = load16_a4(w), a1 = load16_a4(w + 16);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { vw[u][j] = (uint32_t)a0[j]; vw[u][4 + j] = (uint32_t)a1[j]; }
+            vw[u][8] = load4_a4(w + 32);
+        }
+        return true;
+    };
+
+    const int t_guess = __builtin_amdgcn_readfirstlane(split * p.tiles_per_split + wave);
+    bool tile_ok = issue(t_guess);
+
+    // Q8_0 of Q, the MFMA A operand: lane row m = n is head n % G, block c,
+    // elements 16hh .. 16hh+15.
+    const int hq = n % G;
+    intx4 qa[NB];
+    {
+        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G + hq) * HD;
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            float x[16];
+            const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 32 * c + 16 * hh);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const floatx4 v4 = src[j];
+                x[4 * j] = v4[0]; x[4 * j + 1] = v4[1]; x[4 * j + 2] = v4[2]; x[4 * j + 3] = v4[3];
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(x[j]));
+            amax = fmaxf(amax, xor32(amax));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int q0 = (int)roundf(x[4 * j] * id), q1 = (int)roundf(x[4 * j + 1] * id);
+                const int q2 = (int)roundf(x[4 * j + 2] * id), q3 = (int)roundf(x[4 * j + 3] * id);
+                qa[c][j] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
+            }
+            if (wave == 0 && hh == 0 && n < G) lds_dq[n][c] = (float)(_Float16)d;
+        }
     }
+
+    int lo, n_kv, t0, n_tiles, tps, n_active;
+    seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
+    float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
+    if (split >= n_active) {
+        if (split == 0 && n_active == 0) {
+            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out_b[i] = 0.0f;
+        }
+        return;
+    }
+    __syncthreads();  // lds_dq
+    // d_q of the heads of output rows i = 0..3 (rows 4hh + i, head (4hh+i) % G)
+    float dq[4][NB];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < NB; ++c) dq[i][c] = lds_dq[(4 * hh + i) % G][c];
+
+    const int tile_lo = t0 + split * tps;
+    int tile_hi = tile_lo + tps;
+    if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
+    int t = tile_lo + wave_u;
+    if (t != t_guess) tile_ok = t < tile_hi ? issue(t) : false;
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    float m_run[G], l_run[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) { m_run[h] = -INFINITY; l_run[h] = 0.0f; }
+    bool first = true;
+
+    for (; t < tile_hi; t += kDecodeWaves) {
+        const int pos0 = t * kTile;
+        if (!tile_ok) {
+            tile_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
+            continue;
+        }
+        const bool row_ok = pos0 + n >= lo && pos0 + n < n_kv;
+        // S = Q8 * K8^T per block, scaled in block order
+        float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[c], kq[c], intx16{}, 0, 0, 0);
+            const uint32_t dbits = (c & 1) ? (kd[c] >> 16) : (kd[c] & 0xffffu);
+            const float dk = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[i] += (float)acc[i] * (dk * dq[i][c]);
+        }
+        // V blocks: dequantise into the f16 LDS tile (rows outside [lo, n_kv) zeroed)
+#pragma unroll
+        for (int u = 0; u < VBL; ++u) {
+            const int c = VBL * hh + u;
+            uint32_t q[8];
+            uint32_t dbits;
+            if ((c & 1) == 0) {
+                dbits = vw[u][0] & 0xffffu;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(vw[u][j + 1], vw[u][j], 2);
+            } else {
+                dbits = vw[u][0] >> 16;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q[j] = vw[u][j + 1];
+            }
+            const float dv = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
+            half8 h[4];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int qi = (int)(int8_t)((q[j] >> (8 * e)) & 0xffu);
+                    h[j >> 1][4 * (j & 1) + e] = row_ok ? (_Float16)((float)qi * dv) : (_Float16)0.0f;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                *reinterpret_cast<half8 *>(vt + n * VROW + 64 * c + 16 * k) = h[k];
+        }
+        const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
+
+        // online softmax per head (log2 domain); this lane holds position n
+        // for the heads (4hh + i) % G
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = row_ok ? sv[i] * p.scale_log2 : -INFINITY;
+        float alpha[G];
+        float pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if ((4 * hh + i) % G == h) mt = fmaxf(mt, sv[i]);
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+            const float m_new = fmaxf(m_run[h], mt);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            alpha[h] = exp2f(m_run[h] - m_use);
+            m_run[h] = m_new;
+            float ls = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if ((4 * hh + i) % G == h) {
+                    pv[i] = exp2f(sv[i] - m_use);
+                    // each (head, position) once over the wave: for g <= 4 both
+                    // halves hold every head, so only half 0 and i < g count
+                    if (G == 8 || (hh == 0 && i < G)) ls += pv[i];
+                }
+            }
+            l_run[h] = l_run[h] * alpha[h] + ls;
+        }
+        // P -> LDS [head][position]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i < G || G == 8) lds_p[wave][(4 * hh + i) % G][n] = (_Float16)pv[i];
+        }
+        if (!first) {
+            const float a = alpha[n % G];
+#pragma unroll
+            for (int d = 0; d < DB; ++d) o[d] *= a;
+        }
+        first = false;
+
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // P^T operand (column n -> head n % G): positions 16kk + 4hh + 0..3
+        // and 16kk + 8 + 4hh + 0..3, the k order the V^T operand uses
+        half8 pb[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const _Float16 *pr = &lds_p[wave][n % G][16 * kk + 4 * hh];
+            const half4 a0 = *reinterpret_cast<const half4 *>(pr);
+            const half4 a1 = *reinterpret_cast<const half4 *>(pr + 8);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { pb[kk][j] = a0[j]; pb[kk][4 + j] = a1[j]; }
+        }
+        half8 va[2][DB];
+        {
+            const int gq = lane >> 4, rr = lane & 15;
+            const uint8_t *vsrc = vt + (4 * (gq >> 1) + (rr >> 2)) * VROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const half4 h = tr16_read(vsrc + (16 * kk + 8 * u) * VROW + 64 * d);
+                        va[kk][d][4 * u + 0] = h[0];
+                        va[kk][d][4 * u + 1] = h[1];
+                        va[kk][d][4 * u + 2] = h[2];
+                        va[kk][d][4 * u + 3] = h[3];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kk][d], pb[kk], o[d], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        tile_ok = next_ok;
+    }
+
+    // per-head sums over all 64 lanes (each position counted once per head)
+    float Lh[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float v = l_run[h];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+        Lh[h] = v;
+    }
+    float m_col = m_run[0], l_col = Lh[0];
+#pragma unroll
+    for (int h = 1; h < G; ++h)
+        if (n % G == h) { m_col = m_run[h]; l_col = Lh[h]; }
+    split_epilogue<HD, G>(o, m_col, l_col, lds_m, lds_l, lds_o, p, b, kvh, split, n_active, out_b,
+                          wave, n, hh);
 }
 
 // Second pass: out = sum_s o_s * 2^(m_s - M) / sum_s l_s * 2^(m_s - M) over
@@ -380,7 +702,10 @@ struct SplitPlan {
 SplitPlan plan_splits(int B, int Hkv, int max_seq_len) {
     const int tiles = (max_seq_len + kTile - 1) / kTile;
     const int heads = B * Hkv;
-    const int wg_target = 1024;
+    // one round of workgroups over the 256 CUs (one 4-wave workgroup per CU
+    // at this register footprint); longer contexts give each wave more tiles,
+    // whose loads the tile loop prefetches one tile ahead
+    const int wg_target = 256;
     int S = (wg_target + heads - 1) / heads;
     if (S < 1) S = 1;
     if (S > 256) S = 256;
@@ -401,7 +726,12 @@ template <int HD, int G>
 static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStream_t s) {
     if (passes & 1) {
         dim3 grid(p.n_splits, Hkv, B);
-        hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
+        if (p.kv_type == SFA_KV_Q8_0) {
+            if constexpr (HD >= 64 && G <= 8)
+                hipLaunchKernelGGL((decode_q8_kernel<HD, G>), grid, dim3(256), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
+        }
     }
     if ((passes & 2) && p.n_splits > 1)
         hipLaunchKernelGGL((decode_merge_kernel<HD, G>), dim3(B * Hkv * G), dim3(kMergeThreads<HD>), 0,
@@ -454,7 +784,9 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     p.scale_log2 = scale * 1.4426950408889634f;
     p.part = static_cast<float *>(workspace);
 
-    if (kv->kv_type != SFA_KV_F16) return SFA_ERR_UNSUPPORTED;
+    p.kv_type = kv->kv_type;
+    if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0) return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type == SFA_KV_Q8_0 && HD < 64) return SFA_ERR_UNSUPPORTED;
     int rc;
     switch (HD) {
     case 32: rc = launch_f16_g<32>(p, G, B, Hkv, passes, stream); break;

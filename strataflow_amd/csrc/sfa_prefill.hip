@@ -40,9 +40,10 @@ struct PrefillParams {
 };
 
 constexpr int kPBN = 64;           // positions per prefill tile
+constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (P <= 2^8)
 
 template <int HD, int G>
-__global__ __launch_bounds__(256) void prefill_f16_kernel(PrefillParams p) {
+__global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     constexpr int KC = HD / 16;
     constexpr int DB = HD / 32;
     constexpr int QB = 128 / G;           // query tokens per workgroup
@@ -52,25 +53,75 @@ __global__ __launch_bounds__(256) void prefill_f16_kernel(PrefillParams p) {
     constexpr int LPT = CHUNKS / 256;     // chunks per thread per tile
     static_assert(CHUNKS % 256 == 0, "tile chunks");
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds_k[kPBN * ROW];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_v[kPBN * ROW];
+    // double-buffered K and V tiles
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * ROW];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kPBN * ROW];
 
     const int qblk = p.n_qblk - 1 - (int)blockIdx.x;  // heaviest blocks first
     const int kvh = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const int n = lane & 31;
     const int hh = lane >> 5;
     const int Hkv = p.n_head_kv;
     const int64_t col_bytes = (int64_t)Hkv * HD * 2;
 
-    // this lane's query row
+    // this lane's query row (MFMA column n): head g of the group, token tq
     const int rho = wave * 32 + n;
     const int g = rho / QB;
     const int tq = qblk * QB + rho % QB;
     const bool row_ok = tq < p.T;
     const int h = kvh * G + g;
     const int qp = p.q_pos0 + tq;
+
+    // the block's kv range
+    const int first_tok = qblk * QB;
+    int last_tok = first_tok + QB - 1;
+    if (last_tok > p.T - 1) last_tok = p.T - 1;
+    const int kv_hi = p.q_pos0 + last_tok;     // inclusive
+    const int q_lo = p.q_pos0 + first_tok;     // smallest query position of the block
+    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
+    const int tile0 = lo / kPBN;
+    const int tile1 = kv_hi / kPBN;             // inclusive
+    const bool block_full = (qblk + 1) * QB <= p.T;
+
+    // cooperative tile loads into registers: chunk i*256 + tid -> row r, 16B chunk c
+    half8 kreg[LPT], vreg[LPT];
+    bool page_ok = false;
+    auto load = [&](int t) {
+        const int pos0 = t * kPBN;
+        const int lp = pos0 / p.page_size;
+        const int32_t pid = __builtin_amdgcn_readfirstlane(lp < p.max_pages ? p.page_table[lp] : -1);
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        page_ok = kb != nullptr && vb != nullptr;
+        if (!page_ok) return;
+        const int64_t base = (int64_t)(pos0 - lp * p.page_size) * col_bytes + (int64_t)kvh * HD * 2;
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int id = i * 256 + tid;
+            const int r = id / CPR, c = id % CPR;
+            const int64_t off = base + (int64_t)r * col_bytes + 16 * c;
+            kreg[i] = *reinterpret_cast<const half8 *>(kb + off);
+            vreg[i] = *reinterpret_cast<const half8 *>(vb + off);
+        }
+    };
+    // registers -> LDS buffer; V rows outside [lo, kv_hi] zeroed (a page's
+    // unwritten tail may hold any bytes), K rows are masked in the scores
+    auto store = [&](int t, int buf) {
+        const int pos0 = t * kPBN;
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int id = i * 256 + tid;
+            const int r = id / CPR, c = id % CPR;
+            const bool ok = page_ok && pos0 + r >= lo && pos0 + r <= kv_hi;
+            *reinterpret_cast<half8 *>(&lds_k[buf][r * ROW + 16 * c]) = page_ok ? kreg[i] : half8{};
+            *reinterpret_cast<half8 *>(&lds_v[buf][r * ROW + 16 * c]) = ok ? vreg[i] : half8{};
+        }
+    };
+
+    load(tile0);
 
     half8 qf[KC];
     {
@@ -90,97 +141,100 @@ __global__ __launch_bounds__(256) void prefill_f16_kernel(PrefillParams p) {
         }
     }
 
-    // the block's kv range
-    int last_tok = (qblk + 1) * QB - 1;
-    if (last_tok > p.T - 1) last_tok = p.T - 1;
-    const int kv_hi = p.q_pos0 + last_tok;     // inclusive
-    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
-    const int tile0 = lo / kPBN;
-    const int tile1 = kv_hi / kPBN;             // inclusive
+    store(tile0, 0);
+    __syncthreads();
 
     floatx16 o[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) o[d] = floatx16{};
     float m_run = -INFINITY, l_run = 0.0f;
+    const int gq = lane >> 4, rr = lane & 15;
+    const int tr_off = (4 * (gq >> 1) + (rr >> 2)) * ROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
 
     for (int t = tile0; t <= tile1; ++t) {
+        const int buf = (t - tile0) & 1;
         const int pos0 = t * kPBN;
-        // cooperative tile load: chunk id = i*256 + tid -> row = id / CPR
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int id = i * 256 + threadIdx.x;
-            const int r = id / CPR, c = id % CPR;
-            const int pp = pos0 + r;
-            half8 kv8 = half8{}, vv8 = half8{};
-            if (pp >= lo && pp <= kv_hi) {
-                const int lp = pp / p.page_size;
-                const int32_t pid = lp < p.max_pages ? p.page_table[lp] : -1;
-                const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
-                const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
-                const int64_t off = (int64_t)(pp - lp * p.page_size) * col_bytes + (int64_t)kvh * HD * 2 + 16 * c;
-                if (kb) kv8 = *reinterpret_cast<const half8 *>(kb + off);
-                if (vb) vv8 = *reinterpret_cast<const half8 *>(vb + off);
-            }
-            *reinterpret_cast<half8 *>(lds_k + r * ROW + 16 * c) = kv8;
-            *reinterpret_cast<half8 *>(lds_v + r * ROW + 16 * c) = vv8;
-        }
-        __syncthreads();
+        if (t < tile1) load(t + 1);  // in flight while this tile computes
+        const uint8_t *kt = lds_k[buf];
+        const uint8_t *vt = lds_v[buf];
 
-        float sv[2][16];
+        // S^T = K * Q^T for the two 32-position blocks, interleaved chains
+        floatx16 s[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb) {
+                const half8 a = *reinterpret_cast<const half8 *>(kt + (32 * pb + n) * ROW + 32 * c + 16 * hh);
+                s[pb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s[pb], 0, 0, 0);
+            }
+        }
+        // masking only where the tile meets the window start, the diagonal
+        // or rows past T
+        const bool edge = pos0 < lo || pos0 + kPBN - 1 > q_lo || !block_full;
         float mt = -INFINITY;
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
-            floatx16 s = floatx16{};
-#pragma unroll
-            for (int c = 0; c < KC; ++c) {
-                const half8 a = *reinterpret_cast<const half8 *>(lds_k + (32 * pb + n) * ROW + 32 * c + 16 * hh);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
-            }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                const bool ok = row_ok && kp >= lo && kp <= qp;
-                sv[pb][i] = ok ? s[i] * p.scale_log2 : -INFINITY;
-                mt = fmaxf(mt, sv[pb][i]);
+                float v = s[pb][i] * p.scale_log2;
+                if (edge) {
+                    const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
+                    v = (row_ok && kp >= lo && kp <= qp) ? v : -INFINITY;
+                }
+                s[pb][i] = v;
+                mt = fmaxf(mt, v);
             }
         }
         mt = fmaxf(mt, xor32(mt));
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = exp2f(m_run - m_use);
-        m_run = m_new;
+        // lazy rescale: keep the reference max until the tile max exceeds it
+        // by 2^8 (P stays <= 256, exact since O and l share the reference)
+        float alpha = 1.0f;
+        if (mt > m_run + kRescaleLog2) {
+            alpha = exp2f(m_run - mt);  // m_run == -inf -> 0
+            m_run = mt;
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         float ls = 0.0f;
         half8 pbv[2][2];
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float e = exp2f(sv[pb][i] - m_use);
+                const float e = exp2f(s[pb][i] - m_use);
                 ls += e;
                 pbv[pb][i >> 3][i & 7] = (_Float16)e;
             }
         }
         l_run = l_run * alpha + ls;
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int d = 0; d < DB; ++d) o[d] *= alpha;
+            for (int d = 0; d < DB; ++d) o[d] *= alpha;
+        }
 
+        // O^T += V^T * P^T, V^T operands by transposed LDS reads
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
+                half8 va[DB];
 #pragma unroll
                 for (int d = 0; d < DB; ++d) {
-                    half8 a;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int r = 32 * pb + 16 * kk + 8 * (j >> 2) + 4 * hh + (j & 3);
-                        a[j] = *reinterpret_cast<const _Float16 *>(lds_v + r * ROW + 2 * (32 * d + n));
+                    for (int u = 0; u < 2; ++u) {
+                        const half4 hv = tr16_read(vt + tr_off + (32 * pb + 16 * kk + 8 * u) * ROW + 64 * d);
+                        va[d][4 * u + 0] = hv[0];
+                        va[d][4 * u + 1] = hv[1];
+                        va[d][4 * u + 2] = hv[2];
+                        va[d][4 * u + 3] = hv[3];
                     }
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pbv[pb][kk], o[d], 0, 0, 0);
                 }
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d], pbv[pb][kk], o[d], 0, 0, 0);
             }
         }
+        if (t < tile1) store(t + 1, buf ^ 1);
+        __syncthreads();
     }
 
     l_run += xor32(l_run);

@@ -126,3 +126,78 @@ def test_decode_rejects_small_workspace(gpu, oracle_mod):
                              c.max_pages, c.t_sl.data_ptr(), None, 1, 100, 0.088, ws.data_ptr(), 16,
                              torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.SFA_ERR_INVALID_ARGUMENT
+
+
+# ---- Q8_0 KV ------------------------------------------------------------------
+# The gate is the ggml-semantics oracle (Q quantised to Q8_0, integer block
+# dots, the reference's own CPU arithmetic for a Q8_0 cache); the float64
+# exact-dequant reading differs from ggml's by the Q quantisation error
+# (about 0.5% rel-L2 at N(0,1) inputs), so against it the bound is 2e-2.
+Q8_EXACT_REL = 2e-2
+Q8_EXACT_ABS = 2e-2
+
+
+def test_decode_q8_golden(gpu, oracle_mod):
+    import torch
+    from strataflow_amd.paged_kv import PagedKV
+    g = golden("attn_q8_gqa4_decode")
+    n_kv, Hkv = g["k_q8"].shape[:2]
+    hd = g["k_q8"].shape[2] // 34 * 32
+    Hq = int(g["n_head"])
+    ps, n_pages = 32, (n_kv + 31) // 32 + 3
+    kp, pt = scatter_columns(g["k_q8"].reshape(n_kv, -1), ps, n_pages, np.random.default_rng(1))
+    vp, _ = scatter_columns(g["v_q8"].reshape(n_kv, -1), ps, n_pages, np.random.default_rng(1))
+    dev = PagedKV(1, Hq, Hkv, hd, 8, ps, n_pages, device=gpu)
+    dev.k[0].copy_(torch.from_numpy(kp))
+    dev.v[0].copy_(torch.from_numpy(vp))
+    q = torch.from_numpy(g["q"]).to(gpu)
+    out = dev.decode(0, q, torch.from_numpy(pt).to(gpu), torch.tensor([n_kv], dtype=torch.int32, device=gpu),
+                     n_kv, scale=float(g["scale"]))
+    out = out.cpu().numpy().reshape(g["exact"].shape)
+    assert_close(out, g["ggml"], what="q8 vs ggml golden")
+    assert_close(out, g["exact"], max_abs=Q8_EXACT_ABS, rel_l2=Q8_EXACT_REL, what="q8 vs exact golden")
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128), (8, 4, 64), (16, 2, 128), (8, 8, 128), (16, 16, 64)])
+@pytest.mark.parametrize("n_kv", [1, 33, 257, 1000])
+def test_decode_q8_shapes(gpu, oracle_mod, shape, n_kv):
+    Hq, Hkv, hd = shape
+    c = Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, page_size=64,
+             kv_type=8, seed=n_kv + hd + 1)
+    out = c.decode()
+    assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 {shape} n_kv={n_kv} vs ggml")
+    assert_close(out, c.oracle(oracle_mod.EXACT), max_abs=Q8_EXACT_ABS, rel_l2=Q8_EXACT_REL,
+                 what=f"q8 {shape} n_kv={n_kv} vs exact")
+
+
+def test_decode_q8_ctx32768(gpu, oracle_mod):
+    # long-context Q8_0 decode, Mixtral shape, batch 1
+    c = Case(oracle_mod, seq_lens=[32768], kv_type=8, seed=44)
+    out = c.decode()
+    ma, rl = assert_close(out, c.oracle(oracle_mod.GGML), what="q8 32k vs ggml")
+    ma2, rl2 = errors(out, c.oracle(oracle_mod.EXACT))
+    print(f"q8 32k: vs ggml max_abs {ma:.2e} rel_l2 {rl:.2e}; vs exact max_abs {ma2:.2e} rel_l2 {rl2:.2e}")
+    assert ma2 <= Q8_EXACT_ABS and rl2 <= Q8_EXACT_REL
+
+
+def test_decode_q8_batch8_varlen(gpu, oracle_mod):
+    # batch 8, lengths uniform in [8k, 32k], one shared page pool
+    lens = np.random.default_rng(45).integers(8192, 32769, 8)
+    c = Case(oracle_mod, seq_lens=lens, kv_type=8, seed=46)
+    out = c.decode(max_seq_len=32768)
+    assert_close(out, c.oracle(oracle_mod.GGML), what="q8 b8 vs ggml")
+
+
+def test_decode_q8_window_and_placement(gpu, oracle_mod):
+    import torch
+    c = Case(oracle_mod, seq_lens=[3000, 700], kv_lo=[1000, 33], kv_type=8, seed=47, extra_pages=4)
+    base = c.decode()
+    assert_close(base, c.oracle(oracle_mod.GGML), what="q8 window vs ggml")
+    perm = np.random.default_rng(3).permutation(c.n_pages).astype(np.int32)
+    k2 = torch.empty_like(c.dev.k[0]); v2 = torch.empty_like(c.dev.v[0])
+    idx = torch.from_numpy(perm).long().to(gpu)
+    k2[idx] = c.dev.k[0]; v2[idx] = c.dev.v[0]
+    c.dev.k[0].copy_(k2); c.dev.v[0].copy_(v2)
+    pt = c.page_table.copy(); valid = pt >= 0; pt[valid] = perm[pt[valid]]
+    c.t_pt = torch.from_numpy(pt).to(gpu)
+    assert np.array_equal(c.decode().view(np.uint32), base.view(np.uint32))
