@@ -44,7 +44,9 @@ struct DecodeParams {
     int max_pages;
     const int32_t *seq_len;
     const int32_t *kv_lo;
-    int n_splits;         // grid.x
+    int n_splits;         // splits per (sequence, kv head)
+    int n_seq;            // B
+    int split_row;        // B * n_splits rounded up to a multiple of 8
     int tiles_per_split;  // minimum tiles per split (host heuristic)
     float scale_log2;     // scale * log2(e)
     float *part;          // [B][Hkv][n_splits][G][HD + 4]
@@ -54,6 +56,21 @@ constexpr int kDecodeWaves = 4;
 // merge kernel block: one thread per dim, at least one full wave
 template <int HD>
 constexpr int kMergeThreads = HD < 64 ? 64 : HD;
+
+// Workgroup -> (split, kv head, sequence).  The grid is 1-D with rows of
+// `split_row` = B * n_splits rounded up to a multiple of 8; workgroup L serves
+// kv head L / split_row and (sequence, split) L % split_row.  Workgroups go to
+// the eight XCDs round-robin (XCD = L % 8), so every kv head of one (sequence,
+// split) lands on the same XCD and shares its L2: Q8_0 rows (136 bytes) of
+// neighbouring kv heads share cache lines.  Returns false for padding slots.
+__device__ inline bool split_coords(const DecodeParams &p, int &split, int &kvh, int &b) {
+    const int L = blockIdx.x;
+    kvh = L / p.split_row;
+    const int j = L - kvh * p.split_row;
+    b = j / p.n_splits;
+    split = j - b * p.n_splits;
+    return b < p.n_seq;
+}
 
 // Active tile range of sequence b: tiles are 32-aligned absolute position
 // blocks [32t, 32t+32) intersecting [lo, n_kv).
@@ -144,9 +161,8 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
     __shared__ float lds_l[kDecodeWaves][G];
     __shared__ float lds_o[kDecodeWaves][G][HD];
 
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.z;
+    int split, kvh, b;
+    if (!split_coords(p, split, kvh, b)) return;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int n = lane & 31;   // MFMA column (head replica) / A-operand row
@@ -363,9 +379,8 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(DecodeParams p) {
     __shared__ float lds_l[kDecodeWaves][G];
     __shared__ float lds_o[kDecodeWaves][G][HD];
 
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.z;
+    int split, kvh, b;
+    if (!split_coords(p, split, kvh, b)) return;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int n = lane & 31;   // tile position (QK) / MFMA column (PV)
@@ -725,7 +740,7 @@ size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
 template <int HD, int G>
 static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStream_t s) {
     if (passes & 1) {
-        dim3 grid(p.n_splits, Hkv, B);
+        dim3 grid(p.split_row * Hkv);
         if (p.kv_type == SFA_KV_Q8_0) {
             if constexpr (HD >= 64 && G <= 8)
                 hipLaunchKernelGGL((decode_q8_kernel<HD, G>), grid, dim3(256), 0, s, p);
@@ -780,6 +795,8 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     p.seq_len = seq_len;
     p.kv_lo = kv_lo;
     p.n_splits = sp.n_splits;
+    p.n_seq = B;
+    p.split_row = (B * sp.n_splits + 7) / 8 * 8;
     p.tiles_per_split = sp.tiles_per_split;
     p.scale_log2 = scale * 1.4426950408889634f;
     p.part = static_cast<float *>(workspace);
