@@ -53,9 +53,26 @@ struct DecodeParams {
 };
 
 constexpr int kDecodeWaves = 4;
+constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold: P <= 2^8
 // merge kernel block: one thread per dim, at least one full wave
 template <int HD>
 constexpr int kMergeThreads = HD < 64 ? 64 : HD;
+
+// Head of MFMA output register i (rows 8(i/4) + 4hh + i%4, row m is head
+// m % g) for the Q8_0 kernel's S = Q * K^T: (4hh + i) % g, a compile-time
+// value for g <= 4.
+template <int G>
+__device__ inline int head_of(int i, int hh) {
+    return G <= 4 ? (i % G) : ((4 * hh + i) % G);
+}
+template <int G>
+__device__ inline float head_val(const float (&arr)[G], int i, int hh) {
+    if constexpr (G <= 4) {
+        return arr[i % G];
+    } else {
+        return hh ? arr[(4 + i) % G] : arr[i % G];
+    }
+}
 
 // Workgroup -> (split, kv head, sequence).  The grid is 1-D with rows of
 // `split_row` = B * n_splits rounded up to a multiple of 8; workgroup L serves
@@ -129,7 +146,7 @@ __device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run,
 #pragma unroll
         for (int w = 0; w < kDecodeWaves; ++w) {
             const float mw = lds_m[w][g];
-            const float wt = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+            const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
             L += lds_l[w][g] * wt;
             O += lds_o[w][g][d] * wt;
         }
@@ -146,7 +163,7 @@ __device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run,
 }
 
 template <int HD, int G>
-__global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
     static_assert(G >= 1 && G <= 32 && (32 % G) == 0, "group size");
     constexpr int KC = HD / 16;          // 16-dim k chunks of the QK MFMA
@@ -159,6 +176,7 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[kDecodeWaves][kTile * VROW];
     __shared__ float lds_m[kDecodeWaves][G];
     __shared__ float lds_l[kDecodeWaves][G];
+    __shared__ __attribute__((aligned(16))) _Float16 lds_q[G * HD];
     __shared__ float lds_o[kDecodeWaves][G][HD];
 
     int split, kvh, b;
@@ -222,22 +240,24 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
     int t = tile_lo + wave_u;
     if (t != t_guess) tile_ok = t < tile_hi ? issue(t) : false;
 
-    // Q^T operand: column n -> head kvh*G + n%G, dims 16c + 8hh .. +8, f16
-    // (the F16 vec_dot_type conversion ggml applies to src1).  Loaded after
-    // the first tile's K/V so both latencies overlap.
-    half8 qf[KC];
+    // Q of the g heads rounded to f16 (the F16 vec_dot_type conversion ggml
+    // applies to src1), staged once per workgroup in LDS; the Q^T operand of
+    // column n (head n % g, dims 16c + 8hh .. +8) is re-read per tile, which
+    // keeps 32 registers free.  Loaded after the first tile's K/V so both
+    // latencies overlap.
     {
-        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G + (n % G)) * HD;
-#pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 16 * c + 8 * hh);
-            const floatx4 x0 = src[0], x1 = src[1];
+        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
+        for (int i = threadIdx.x; i < G * HD / 8; i += blockDim.x) {
+            const floatx4 x0 = reinterpret_cast<const floatx4 *>(qr)[2 * i];
+            const floatx4 x1 = reinterpret_cast<const floatx4 *>(qr)[2 * i + 1];
             half8 h;
             h[0] = (_Float16)x0[0]; h[1] = (_Float16)x0[1]; h[2] = (_Float16)x0[2]; h[3] = (_Float16)x0[3];
             h[4] = (_Float16)x1[0]; h[5] = (_Float16)x1[1]; h[6] = (_Float16)x1[2]; h[7] = (_Float16)x1[3];
-            qf[c] = h;
+            reinterpret_cast<half8 *>(lds_q)[i] = h;
         }
     }
+    __syncthreads();
+    const half8 *qrow = reinterpret_cast<const half8 *>(lds_q) + (n % G) * (HD / 8) + hh;
 
     floatx16 o[DB];
 #pragma unroll
@@ -252,13 +272,10 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
             tile_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
             continue;
         }
-        // S^T = K * Q^T, two accumulation chains
-        floatx16 s0 = floatx16{}, s1 = floatx16{};
+        // S^T = K * Q^T
+        floatx16 s0 = floatx16{};
 #pragma unroll
-        for (int c = 0; c < KC; c += 2) {
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s0, 0, 0, 0);
-            if (c + 1 < KC) s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c + 1], qf[c + 1], s1, 0, 0, 0);
-        }
+        for (int c = 0; c < KC; ++c) s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qrow[2 * c], s0, 0, 0, 0);
         // V tile into the wave's LDS region; rows outside [lo, n_kv) zeroed
         // (they may hold stale bytes of a page's unused tail)
 #pragma unroll
@@ -271,36 +288,45 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
         const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
 
         // online softmax (log2 domain); row of register i is tile position
-        // 8(i/4) + 4hh + i%4
+        // 8(i/4) + 4hh + i%4.  Interior tiles need no mask.  The reference
+        // max moves only when a score exceeds it by 2^8 (a wave-uniform
+        // ballot), so most tiles skip the max exchange and the O rescale;
+        // P <= 256 and O, l share the reference, so the result is unchanged.
+        const bool interior = pos0 >= lo && pos0 + kTile <= n_kv;
         float sv[16];
         float mt = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int r = 8 * (i >> 2) + 4 * hh + (i & 3);
-            const int pp = pos0 + r;
-            const bool ok = pp >= lo && pp < n_kv;
-            sv[i] = ok ? (s0[i] + s1[i]) * p.scale_log2 : -INFINITY;
-            mt = fmaxf(mt, sv[i]);
+            float v = s0[i] * p.scale_log2;
+            if (!interior) {
+                const int pp = pos0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                v = (pp >= lo && pp < n_kv) ? v : -INFINITY;
+            }
+            sv[i] = v;
+            mt = fmaxf(mt, v);
         }
-        mt = fmaxf(mt, xor32(mt));
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = exp2f(m_run - m_use);
+        if (__any(mt > m_run + kRescaleLog2)) {
+            mt = fmaxf(mt, xor32(mt));
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run == -inf -> 0
+            l_run *= alpha;
+            if (!first) {
+#pragma unroll
+                for (int d = 0; d < DB; ++d) o[d] *= alpha;
+            }
+            m_run = m_new;
+        }
+        first = false;
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         float ls = 0.0f;
         half8 pb[2];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float e = exp2f(sv[i] - m_use);
+            const float e = __builtin_amdgcn_exp2f(sv[i] - m_use);
             ls += e;
             pb[i >> 3][i & 7] = (_Float16)e;
         }
-        l_run = l_run * alpha + ls;
-        m_run = m_new;
-        if (!first) {  // o is still zero on the first tile
-#pragma unroll
-            for (int d = 0; d < DB; ++d) o[d] *= alpha;
-        }
-        first = false;
+        l_run += ls;
 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -313,30 +339,27 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
         // r of group gq supplies chunk (position 16kk + 8u + 4(gq/2) + r/4,
         // dims 32d + 16(gq%2) + 4(r%4)) and receives its own dim n at the four
         // positions of half u.
-        half8 va[2][DB];
         {
             const int gq = lane >> 4, rr = lane & 15;
             const uint8_t *vsrc = vt + (4 * (gq >> 1) + (rr >> 2)) * VROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
+                half8 va[DB];
 #pragma unroll
                 for (int d = 0; d < DB; ++d) {
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
                         const half4 h = tr16_read(vsrc + (16 * kk + 8 * u) * VROW + 64 * d);
-                        va[kk][d][4 * u + 0] = h[0];
-                        va[kk][d][4 * u + 1] = h[1];
-                        va[kk][d][4 * u + 2] = h[2];
-                        va[kk][d][4 * u + 3] = h[3];
+                        va[d][4 * u + 0] = h[0];
+                        va[d][4 * u + 1] = h[1];
+                        va[d][4 * u + 2] = h[2];
+                        va[d][4 * u + 3] = h[3];
                     }
                 }
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d], pb[kk], o[d], 0, 0, 0);
             }
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-            for (int d = 0; d < DB; ++d)
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kk][d], pb[kk], o[d], 0, 0, 0);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -364,7 +387,7 @@ __global__ __launch_bounds__(256) void decode_f16_kernel(DecodeParams p) {
 //     LDS tile layout as the f16 path, and P goes through LDS to the P^T
 //     operand; PV is the f16 path's O^T = V^T * P^T.
 template <int HD, int G>
-__global__ __launch_bounds__(256) void decode_q8_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodeParams p) {
     static_assert(HD == 64 || HD == 128, "head_dim");
     static_assert(G >= 1 && G <= 8 && (8 % G) == 0, "group size");
     constexpr int NB = HD / 32;          // blocks per row
@@ -500,9 +523,9 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(DecodeParams p) {
     floatx16 o[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) o[d] = floatx16{};
-    float m_run[G], l_run[G];
+    float m_run[G], l_run[G], alpha_h[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h) { m_run[h] = -INFINITY; l_run[h] = 0.0f; }
+    for (int h = 0; h < G; ++h) { m_run[h] = -INFINITY; l_run[h] = 0.0f; alpha_h[h] = 1.0f; }
     bool first = true;
 
     for (; t < tile_hi; t += kDecodeWaves) {
@@ -512,6 +535,7 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(DecodeParams p) {
             continue;
         }
         const bool row_ok = pos0 + n >= lo && pos0 + n < n_kv;
+        const bool interior = pos0 >= lo && pos0 + kTile <= n_kv;
         // S = Q8 * K8^T per block, scaled in block order
         float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -544,7 +568,7 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(DecodeParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int qi = (int)(int8_t)((q[j] >> (8 * e)) & 0xffu);
-                    h[j >> 1][4 * (j & 1) + e] = row_ok ? (_Float16)((float)qi * dv) : (_Float16)0.0f;
+                    h[j >> 1][4 * (j & 1) + e] = (interior || row_ok) ? (_Float16)((float)qi * dv) : (_Float16)0.0f;
                 }
             }
 #pragma unroll
@@ -554,46 +578,58 @@ __global__ __launch_bounds__(256) void decode_q8_kernel(DecodeParams p) {
         const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
 
         // online softmax per head (log2 domain); this lane holds position n
-        // for the heads (4hh + i) % G
+        // for the heads (4hh + i) % G of registers i = 0..3 (i % G when
+        // g <= 4).  Lazy reference max as in the f16 path.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = row_ok ? sv[i] * p.scale_log2 : -INFINITY;
-        float alpha[G];
-        float pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 4; ++i) sv[i] = (interior || row_ok) ? sv[i] * p.scale_log2 : -INFINITY;
+        bool exceed = false;
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float mt = -INFINITY;
+        for (int i = 0; i < 4; ++i) exceed |= sv[i] > head_val(m_run, i, hh) + kRescaleLog2;
+        if (__any(exceed)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if ((4 * hh + i) % G == h) mt = fmaxf(mt, sv[i]);
+            for (int h = 0; h < G; ++h) {
+                float mt = -INFINITY;
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
-            const float m_new = fmaxf(m_run[h], mt);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            alpha[h] = exp2f(m_run[h] - m_use);
-            m_run[h] = m_new;
-            float ls = 0.0f;
+                for (int i = 0; i < 4; ++i)
+                    if (head_of<G>(i, hh) == h) mt = fmaxf(mt, sv[i]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if ((4 * hh + i) % G == h) {
-                    pv[i] = exp2f(sv[i] - m_use);
-                    // each (head, position) once over the wave: for g <= 4 both
-                    // halves hold every head, so only half 0 and i < g count
-                    if (G == 8 || (hh == 0 && i < G)) ls += pv[i];
-                }
+                for (int off = 1; off < 64; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+                const float m_new = fmaxf(m_run[h], mt);
+                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);  // m_run == -inf -> 0
+                l_run[h] *= alpha;
+                alpha_h[h] = alpha;
+                m_run[h] = m_new;
             }
-            l_run[h] = l_run[h] * alpha[h] + ls;
+            if (!first) {
+                float a = alpha_h[0];
+#pragma unroll
+                for (int h = 1; h < G; ++h) a = (n % G == h) ? alpha_h[h] : a;
+#pragma unroll
+                for (int d = 0; d < DB; ++d) o[d] *= a;
+            }
+        }
+        first = false;
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float mr = head_val(m_run, i, hh);
+            pv[i] = __builtin_amdgcn_exp2f(sv[i] - (mr == -INFINITY ? 0.0f : mr));
+        }
+        // each (head, position) counted once over the wave: for g <= 4 both
+        // halves hold every head, so only half 0 and i < g count
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (G == 8) {
+                if (hh) l_run[4 + i] += pv[i]; else l_run[i] += pv[i];
+            } else if (i < G && hh == 0) {
+                l_run[i] += pv[i];
+            }
         }
         // P -> LDS [head][position]
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (i < G || G == 8) lds_p[wave][(4 * hh + i) % G][n] = (_Float16)pv[i];
+            if (i < G || G == 8) lds_p[wave][head_of<G>(i, hh)][n] = (_Float16)pv[i];
         }
-        if (!first) {
-            const float a = alpha[n % G];
-#pragma unroll
-            for (int d = 0; d < DB; ++d) o[d] *= a;
-        }
-        first = false;
 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -692,12 +728,12 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
         for (int u = 0; u < CH; ++u)
             if (s0 + u < n_active) mc = fmaxf(mc, m[u]);
         if (mc == -INFINITY) continue;
-        const float a = exp2f(M - mc);  // M == -inf -> 0
+        const float a = __builtin_amdgcn_exp2f(M - mc);  // M == -inf -> 0
         L *= a;
         O *= a;
 #pragma unroll
         for (int u = 0; u < CH; ++u) {
-            const float w = (s0 + u < n_active && m[u] != -INFINITY) ? exp2f(m[u] - mc) : 0.0f;
+            const float w = (s0 + u < n_active && m[u] != -INFINITY) ? __builtin_amdgcn_exp2f(m[u] - mc) : 0.0f;
             L += l[u] * w;
             O += o[u] * w;
         }
@@ -717,10 +753,10 @@ struct SplitPlan {
 SplitPlan plan_splits(int B, int Hkv, int max_seq_len) {
     const int tiles = (max_seq_len + kTile - 1) / kTile;
     const int heads = B * Hkv;
-    // one round of workgroups over the 256 CUs (one 4-wave workgroup per CU
-    // at this register footprint); longer contexts give each wave more tiles,
-    // whose loads the tile loop prefetches one tile ahead
-    const int wg_target = 256;
+    // one round of workgroups: two 4-wave workgroups per CU (two waves per
+    // SIMD at these register footprints) over 256 CUs; longer contexts give
+    // each wave more tiles, whose loads the tile loop prefetches one ahead
+    const int wg_target = 512;
     int S = (wg_target + heads - 1) / heads;
     if (S < 1) S = 1;
     if (S > 256) S = 256;

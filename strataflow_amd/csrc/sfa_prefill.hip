@@ -53,12 +53,21 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     constexpr int LPT = CHUNKS / 256;     // chunks per thread per tile
     static_assert(CHUNKS % 256 == 0, "tile chunks");
 
-    // double-buffered K and V tiles
-    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * ROW];
+    // double-buffered K and V tiles.  K rows are unpadded with the 16-byte
+    // chunk c of row r stored at chunk c ^ (r % CPR), so the 32 rows an MFMA
+    // operand read touches spread over all banks; V rows are padded (the
+    // transposed reads walk rows).
+    constexpr int KROW = HD * 2;
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * KROW];
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kPBN * ROW];
 
-    const int qblk = p.n_qblk - 1 - (int)blockIdx.x;  // heaviest blocks first
-    const int kvh = blockIdx.y;
+    // 1-D grid: workgroup L serves kv head L % Hkv and query block
+    // n_qblk - 1 - L / Hkv (heaviest blocks first).  Workgroups go to the
+    // eight XCDs round-robin (XCD = L % 8), so with Hkv a multiple of 8 every
+    // query block of one kv head runs on one XCD and that head's K/V stays in
+    // its L2 (each tile is re-read by every query block of the head).
+    const int kvh = (int)blockIdx.x % p.n_head_kv;
+    const int qblk = p.n_qblk - 1 - (int)blockIdx.x / p.n_head_kv;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -116,7 +125,7 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
             const int id = i * 256 + tid;
             const int r = id / CPR, c = id % CPR;
             const bool ok = page_ok && pos0 + r >= lo && pos0 + r <= kv_hi;
-            *reinterpret_cast<half8 *>(&lds_k[buf][r * ROW + 16 * c]) = page_ok ? kreg[i] : half8{};
+            *reinterpret_cast<half8 *>(&lds_k[buf][r * KROW + 16 * (c ^ (r % CPR))]) = page_ok ? kreg[i] : half8{};
             *reinterpret_cast<half8 *>(&lds_v[buf][r * ROW + 16 * c]) = ok ? vreg[i] : half8{};
         }
     };
@@ -164,33 +173,36 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         for (int c = 0; c < KC; ++c) {
 #pragma unroll
             for (int pb = 0; pb < 2; ++pb) {
-                const half8 a = *reinterpret_cast<const half8 *>(kt + (32 * pb + n) * ROW + 32 * c + 16 * hh);
+                const int r = 32 * pb + n;
+                const half8 a = *reinterpret_cast<const half8 *>(kt + r * KROW + 16 * ((2 * c + hh) ^ (r % CPR)));
                 s[pb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s[pb], 0, 0, 0);
             }
         }
         // masking only where the tile meets the window start, the diagonal
-        // or rows past T
+        // or rows past T (wave-uniform branch)
         const bool edge = pos0 < lo || pos0 + kPBN - 1 > q_lo || !block_full;
-        float mt = -INFINITY;
+        if (edge) {
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
+            for (int pb = 0; pb < 2; ++pb) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float v = s[pb][i] * p.scale_log2;
-                if (edge) {
+                for (int i = 0; i < 16; ++i) {
                     const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                    v = (row_ok && kp >= lo && kp <= qp) ? v : -INFINITY;
+                    s[pb][i] = (row_ok && kp >= lo && kp <= qp) ? s[pb][i] : -INFINITY;
                 }
-                s[pb][i] = v;
-                mt = fmaxf(mt, v);
             }
         }
-        mt = fmaxf(mt, xor32(mt));
+        // raw scores; the scale (> 0) is applied inside the exponent
+        float mt = -INFINITY;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
+        mt = fmaxf(mt, xor32(mt)) * p.scale_log2;
         // lazy rescale: keep the reference max until the tile max exceeds it
         // by 2^8 (P stays <= 256, exact since O and l share the reference)
         float alpha = 1.0f;
         if (mt > m_run + kRescaleLog2) {
-            alpha = exp2f(m_run - mt);  // m_run == -inf -> 0
+            alpha = __builtin_amdgcn_exp2f(m_run - mt);  // m_run == -inf -> 0
             m_run = mt;
         }
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
@@ -200,7 +212,7 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         for (int pb = 0; pb < 2; ++pb) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float e = exp2f(s[pb][i] - m_use);
+                const float e = __builtin_amdgcn_exp2f(fmaf(s[pb][i], p.scale_log2, -m_use));
                 ls += e;
                 pbv[pb][i >> 3][i & 7] = (_Float16)e;
             }
@@ -253,7 +265,7 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
 
 template <int HD, int G>
 static void launch_prefill(const PrefillParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((prefill_f16_kernel<HD, G>), dim3(p.n_qblk, p.n_head_kv), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((prefill_f16_kernel<HD, G>), dim3(p.n_qblk * p.n_head_kv), dim3(256), 0, s, p);
 }
 
 template <int HD>
