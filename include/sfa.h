@@ -108,8 +108,8 @@ SFA_API int sfa_kv_append(const sfa_kv_desc *kv, const float *k, const float *v,
                           const int32_t *page_table, int32_t max_pages,
                           void *stream);
 
-/* Workspace bytes needed by sfa_attn_decode for B sequences whose seq_len never
- * exceeds max_seq_len. */
+/* Workspace bytes needed by sfa_attn_decode for B sequences with the given
+ * max_seq_len (the bound on the attended span, see sfa_attn_decode). */
 SFA_API size_t sfa_decode_workspace_bytes(const sfa_kv_desc *kv, int32_t B,
                                           int32_t max_seq_len);
 
@@ -126,7 +126,10 @@ SFA_API int sfa_workspace_init(void *workspace, size_t ws_bytes, void *stream);
  *           the reference semantics: every position 0..n_kv-1 is attended
  *           (the KV window bounds residency only, src/kv/kv_store.h:1-22).  A
  *           positive kv_lo is an opt-in sliding attention window.
- *   max_seq_len : host bound on every seq_len[b] (sizes the split grid)
+ *   max_seq_len : host bound on every attended span seq_len[b] - kv_lo[b]
+ *           (seq_len[b] when kv_lo is NULL); sizes the split grid and the
+ *           workspace.  A longer span is still attended in full, by fewer,
+ *           longer splits.
  *   scale : 1/sqrt(head_dim) in the reference (engine.cpp:1756)
  * Split-K over logical positions, then a merge pass in split order: results
  * do not depend on where pages live (paged == contiguous, bit for bit).

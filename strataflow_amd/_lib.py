@@ -118,3 +118,93 @@ def status_str(status: int) -> str:
 def check(status: int, what: str) -> None:
     if status != SFA_OK:
         raise SfaError(status, what)
+
+
+# ---- libsfa_host.so (include/sfa_pager.h) -----------------------------------
+
+HOST_LIB_PATH = Path(__file__).resolve().parent / "libsfa_host.so"
+
+SFA_ATTEND_LOSSLESS = 0
+SFA_ATTEND_WINDOW = 1
+
+#: every symbol include/sfa_pager.h declares
+HOST_EXPORTS = (
+    "sfa_pager_create",
+    "sfa_pager_destroy",
+    "sfa_pager_begin",
+    "sfa_pager_append",
+    "sfa_pager_attend",
+    "sfa_pager_reset",
+    "sfa_pager_stats_get",
+    "sfa_pager_desc",
+    "sfa_pager_max_pages",
+    "sfa_pager_tables",
+)
+
+
+class SfaPagerConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_layer", ctypes.c_int32),
+        ("n_head", ctypes.c_int32),
+        ("n_head_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("kv_type", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("n_seq", ctypes.c_int32),
+        ("n_ctx", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("attend", ctypes.c_int32),
+        ("n_pages", ctypes.c_int32),
+        ("n_cold_pages", ctypes.c_int32),
+        ("seed", ctypes.c_uint64),
+    ]
+
+
+class SfaPagerStats(ctypes.Structure):
+    _fields_ = [
+        ("pages_allocated", ctypes.c_int64),
+        ("pages_evicted", ctypes.c_int64),
+        ("pages_dropped", ctypes.c_int64),
+        ("dev_pages_in_use", ctypes.c_int64),
+        ("cold_pages_in_use", ctypes.c_int64),
+        ("bytes_evicted", ctypes.c_int64),
+    ]
+
+
+_host = None
+
+
+def load_host(path: Path | str | None = None) -> ctypes.CDLL:
+    """Loads libsfa_host.so (once; it loads libsfa.so next to it)."""
+    global _host
+    if _host is not None:
+        return _host
+    load()
+    p = Path(path or os.environ.get("SFA_HOST_LIB", HOST_LIB_PATH))
+    if not p.exists():
+        raise RuntimeError(f"{p} is missing: build it first (python -m strataflow_amd.build)")
+    lib = ctypes.CDLL(str(p))
+    P = ctypes.c_void_p
+    i32 = ctypes.c_int32
+    lib.sfa_pager_create.argtypes = [ctypes.POINTER(SfaPagerConfig), ctypes.POINTER(P)]
+    lib.sfa_pager_create.restype = ctypes.c_int
+    lib.sfa_pager_destroy.argtypes = [P]
+    lib.sfa_pager_destroy.restype = None
+    lib.sfa_pager_begin.argtypes = [P, P, P]
+    lib.sfa_pager_begin.restype = ctypes.c_int
+    lib.sfa_pager_append.argtypes = [P, i32, P, P, P]
+    lib.sfa_pager_append.restype = ctypes.c_int
+    lib.sfa_pager_attend.argtypes = [P, i32, P, P, P]
+    lib.sfa_pager_attend.restype = ctypes.c_int
+    lib.sfa_pager_reset.argtypes = [P, i32, P]
+    lib.sfa_pager_reset.restype = ctypes.c_int
+    lib.sfa_pager_stats_get.argtypes = [P, ctypes.POINTER(SfaPagerStats)]
+    lib.sfa_pager_stats_get.restype = ctypes.c_int
+    lib.sfa_pager_desc.argtypes = [P, i32, ctypes.POINTER(SfaKvDesc)]
+    lib.sfa_pager_desc.restype = ctypes.c_int
+    lib.sfa_pager_max_pages.argtypes = [P]
+    lib.sfa_pager_max_pages.restype = i32
+    lib.sfa_pager_tables.argtypes = [P, P, P]
+    lib.sfa_pager_tables.restype = ctypes.c_int
+    _host = lib
+    return lib

@@ -1,8 +1,9 @@
 """Builds libsfa.so (the gfx950 HIP library) and the CPU oracle in-tree.
 
 ``python -m strataflow_amd.build`` compiles every ``csrc/*.hip`` with hipcc for
-gfx950 only and links ``strataflow_amd/libsfa.so``; it also builds
-``oracle/liboracle.so`` (the test-side checker) with make.
+gfx950 only and links ``strataflow_amd/libsfa.so`` (the attention library);
+``host/`` (the C++ page manager over it) becomes ``strataflow_amd/libsfa_host.so``;
+it also builds ``oracle/liboracle.so`` (the test-side checker) with make.
 """
 from __future__ import annotations
 
@@ -16,8 +17,10 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
+HOST = PKG / "host"
 OBJ = ROOT / "_build" / "obj"
 LIB = PKG / "libsfa.so"
+HOST_LIB = PKG / "libsfa_host.so"
 ORACLE_DIR = ROOT / "oracle"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -68,6 +71,32 @@ def build_hip(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_host(verbose: bool = False) -> Path:
+    """The host page manager: plain C++ with g++, the HIP part with hipcc,
+    linked against libsfa.so (found next to it at run time)."""
+    OBJ.mkdir(parents=True, exist_ok=True)
+    objs = []
+    for src in sorted(HOST.glob("*.cpp")):
+        obj = OBJ / ("host_" + src.stem + ".o")
+        cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{HOST}", "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), file=sys.stderr)
+        _run(cmd)
+        objs.append(obj)
+    for src in sorted(HOST.glob("*.hip")):
+        obj = OBJ / ("host_" + src.stem + ".o")
+        cmd = [HIPCC, *HIP_FLAGS, f"-I{HOST}", "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), file=sys.stderr)
+        _run(cmd)
+        objs.append(obj)
+    tmp = HOST_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+          f"-L{PKG}", "-lsfa", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
+
+
 def build_oracle() -> Path:
     make = shutil.which("make")
     if make is None:
@@ -78,6 +107,7 @@ def build_oracle() -> Path:
 
 def build_all(verbose: bool = False) -> None:
     build_hip(verbose)
+    build_host(verbose)
     build_oracle()
 
 

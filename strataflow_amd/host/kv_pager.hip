@@ -1,0 +1,359 @@
+// kv_pager.hip - host-side paged KV manager over libsfa.so (sfa_pager.h).
+//
+// Owns the device pool of every layer's K and V pages, the host-pinned cold
+// pool and the device page tables; PagePlanner decides residency and this file
+// carries its decisions out on one stream: eviction copies (one strided
+// device-to-host copy moves a page of every layer, K and V), then one small
+// kernel that applies the page-table edits and writes seq_len, kv_lo and the
+// step's (seq, pos) token arrays.  Step metadata travels as kernel arguments,
+// so a step needs no host staging buffer and no synchronisation.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <map>
+#include <new>
+#include <vector>
+
+#include "page_planner.h"
+#include "sfa.h"
+#include "sfa_pager.h"
+
+namespace {
+
+constexpr int kUpdSeqs = 32;    // sequences per update launch
+constexpr int kUpdEdits = 128;  // page-table edits per update launch
+
+struct StepArgs {
+    int32_t *table;
+    int32_t *seq_len;
+    int32_t *kv_lo;
+    int32_t *tok_seq;
+    int32_t *tok_pos;
+    int32_t n_seq;
+    int32_t n_edit;
+    int32_t seq[kUpdSeqs];
+    int32_t tok_off[kUpdSeqs];
+    int32_t pos0[kUpdSeqs];
+    int32_t n_tok[kUpdSeqs];
+    int32_t len[kUpdSeqs];
+    int32_t lo[kUpdSeqs];
+    int32_t edit_idx[kUpdEdits];
+    int32_t edit_val[kUpdEdits];
+};
+
+__global__ __launch_bounds__(256) void step_update_kernel(StepArgs a) {
+    const int t = threadIdx.x;
+    for (int i = t; i < a.n_edit; i += blockDim.x) a.table[a.edit_idx[i]] = a.edit_val[i];
+    for (int s = 0; s < a.n_seq; ++s) {
+        if (t == 0) {
+            a.seq_len[a.seq[s]] = a.len[s];
+            a.kv_lo[a.seq[s]] = a.lo[s];
+        }
+        for (int i = t; i < a.n_tok[s]; i += blockDim.x) {
+            a.tok_seq[a.tok_off[s] + i] = a.seq[s];
+            a.tok_pos[a.tok_off[s] + i] = a.pos0[s] + i;
+        }
+    }
+}
+
+inline hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+struct sfa_pager {
+    sfa_pager_config cfg{};
+    sfa::PagePlanner planner;
+    size_t page_bytes = 0;
+    int max_pages = 0;
+    int32_t max_span = 0;
+    uint8_t *dev_pool = nullptr;   // [layer][K|V][n_pages][page_bytes]
+    uint8_t *cold_pool = nullptr;  // [layer][K|V][n_cold][page_bytes], host-pinned
+    int32_t *d_table = nullptr;    // [n_seq][max_pages]
+    int32_t *d_seq_len = nullptr;  // [n_seq]
+    int32_t *d_kv_lo = nullptr;    // [n_seq]
+    int32_t *d_tok_seq = nullptr;  // [n_seq * page_size]
+    int32_t *d_tok_pos = nullptr;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    std::vector<sfa_kv_desc> descs;
+    // the current step
+    std::vector<int32_t> step_ntok, step_pos0, step_off;
+    int32_t step_tokens = 0;
+    bool step_open = false;
+    int64_t bytes_evicted = 0;
+
+    sfa_pager(const sfa_pager_config &c, int n_pages, int n_cold)
+        : cfg(c),
+          planner(c.n_seq, c.page_size, (uint32_t)c.n_ctx, (uint32_t)c.window, n_pages, n_cold,
+                  c.attend == SFA_ATTEND_LOSSLESS, c.seed) {}
+
+    ~sfa_pager() {
+        if (dev_pool) (void)hipFree(dev_pool);
+        if (cold_pool) (void)hipHostFree(cold_pool);
+        for (int32_t *p : {d_table, d_seq_len, d_kv_lo, d_tok_seq, d_tok_pos})
+            if (p) (void)hipFree(p);
+        if (ws) (void)hipFree(ws);
+    }
+
+    int n_pages() const { return cfg.n_pages; }
+    int n_cold() const { return cfg.n_cold_pages; }
+
+    int launch_updates(const std::vector<std::pair<int32_t, int32_t>> &edits, hipStream_t s) {
+        const int n_seq = cfg.n_seq;
+        size_t e = 0;
+        int b = 0;
+        do {
+            StepArgs a{};
+            a.table = d_table;
+            a.seq_len = d_seq_len;
+            a.kv_lo = d_kv_lo;
+            a.tok_seq = d_tok_seq;
+            a.tok_pos = d_tok_pos;
+            for (; a.n_seq < kUpdSeqs && b < n_seq; ++b, ++a.n_seq) {
+                const int i = a.n_seq;
+                a.seq[i] = b;
+                a.tok_off[i] = step_off[b];
+                a.pos0[i] = step_pos0[b];
+                a.n_tok[i] = step_ntok[b];
+                a.len[i] = (int32_t)planner.store(b).used();
+                a.lo[i] = (int32_t)planner.attend_lo(b);
+            }
+            for (; a.n_edit < kUpdEdits && e < edits.size(); ++e, ++a.n_edit) {
+                a.edit_idx[a.n_edit] = edits[e].first;
+                a.edit_val[a.n_edit] = edits[e].second;
+            }
+            hipLaunchKernelGGL(step_update_kernel, dim3(1), dim3(256), 0, s, a);
+            if (hipGetLastError() != hipSuccess) return SFA_ERR_RUNTIME;
+        } while (b < n_seq || e < edits.size());
+        return SFA_OK;
+    }
+
+    int apply(const std::vector<sfa::PageAction> &actions, hipStream_t s) {
+        const size_t slab = (size_t)2 * cfg.n_layer;  // (layer, K|V) rows of a page
+        std::map<int32_t, int32_t> edits;              // table slot -> final id
+        for (const sfa::PageAction &a : actions) {
+            if (a.kind == sfa::PageAction::kEvict) {
+                // page `dev` of every (layer, K|V) pool -> cold page `cold`
+                if (hipMemcpy2DAsync(cold_pool + (size_t)a.cold * page_bytes,
+                                     (size_t)n_cold() * page_bytes,
+                                     dev_pool + (size_t)a.dev * page_bytes,
+                                     (size_t)n_pages() * page_bytes, page_bytes, slab,
+                                     hipMemcpyDeviceToHost, s) != hipSuccess)
+                    return SFA_ERR_RUNTIME;
+                bytes_evicted += (int64_t)(page_bytes * slab);
+            }
+            const int32_t slot = a.seq * max_pages + a.lpage;
+            edits[slot] = planner.table()[slot];
+        }
+        std::vector<std::pair<int32_t, int32_t>> list(edits.begin(), edits.end());
+        return launch_updates(list, s);
+    }
+};
+
+extern "C" {
+
+SFA_API int sfa_pager_create(const sfa_pager_config *cfg_in, sfa_pager **out) {
+    if (cfg_in == nullptr || out == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    sfa_pager_config c = *cfg_in;
+    if (c.n_layer <= 0 || c.n_seq <= 0 || c.n_ctx <= 0 || c.page_size <= 0 || c.window < 0)
+        return SFA_ERR_INVALID_ARGUMENT;
+    if (c.attend != SFA_ATTEND_LOSSLESS && c.attend != SFA_ATTEND_WINDOW)
+        return SFA_ERR_INVALID_ARGUMENT;
+    if (c.window == 0 || c.window > c.n_ctx) c.window = c.n_ctx;
+    const int max_pages = (c.n_ctx + c.page_size - 1) / c.page_size;
+    const int win_pages = (c.window + c.page_size - 1) / c.page_size + 1;
+    if (c.n_pages <= 0) c.n_pages = c.n_seq * std::min(win_pages, max_pages);
+    const bool paging = c.window < c.n_ctx;
+    if (c.attend == SFA_ATTEND_LOSSLESS && paging) {
+        if (c.n_cold_pages <= 0) c.n_cold_pages = c.n_seq * max_pages;
+    } else {
+        c.n_cold_pages = 0;
+    }
+
+    sfa_kv_desc d{};
+    d.n_head = c.n_head;
+    d.n_head_kv = c.n_head_kv;
+    d.head_dim = c.head_dim;
+    d.page_size = c.page_size;
+    d.kv_type = c.kv_type;
+    if (int rc = sfa_kv_desc_check(&d); rc != SFA_OK) return rc;  // shapes (no pools yet)
+    d.n_pages = c.n_pages;
+
+    sfa_pager *p = nullptr;
+    try {
+        p = new sfa_pager(c, c.n_pages, c.n_cold_pages);
+        p->page_bytes = sfa_page_bytes(&d);
+        p->max_pages = max_pages;
+        p->max_span = c.attend == SFA_ATTEND_WINDOW ? c.window : c.n_ctx;
+        p->step_ntok.assign(c.n_seq, 0);
+        p->step_pos0.assign(c.n_seq, 0);
+        p->step_off.assign(c.n_seq, 0);
+    } catch (const std::bad_alloc &) {
+        delete p;
+        return SFA_ERR_OUT_OF_MEMORY;
+    }
+    auto fail = [&](int rc) {
+        delete p;
+        return rc;
+    };
+    const size_t slab = (size_t)2 * c.n_layer;
+    if (hipMalloc(&p->dev_pool, slab * c.n_pages * p->page_bytes) != hipSuccess)
+        return fail(SFA_ERR_OUT_OF_MEMORY);
+    if (c.n_cold_pages > 0 &&
+        hipHostMalloc(reinterpret_cast<void **>(&p->cold_pool), slab * c.n_cold_pages * p->page_bytes,
+                      hipHostMallocDefault) != hipSuccess)
+        return fail(SFA_ERR_OUT_OF_MEMORY);
+    const size_t n_table = (size_t)c.n_seq * max_pages;
+    const size_t n_tok = (size_t)c.n_seq * c.page_size;
+    if (hipMalloc(&p->d_table, n_table * 4) != hipSuccess ||
+        hipMalloc(&p->d_seq_len, (size_t)c.n_seq * 4) != hipSuccess ||
+        hipMalloc(&p->d_kv_lo, (size_t)c.n_seq * 4) != hipSuccess ||
+        hipMalloc(&p->d_tok_seq, n_tok * 4) != hipSuccess ||
+        hipMalloc(&p->d_tok_pos, n_tok * 4) != hipSuccess)
+        return fail(SFA_ERR_OUT_OF_MEMORY);
+    // empty tables (-1), zero lengths; the pools need no initial contents
+    if (hipMemset(p->d_table, 0xFF, n_table * 4) != hipSuccess ||
+        hipMemset(p->d_seq_len, 0, (size_t)c.n_seq * 4) != hipSuccess ||
+        hipMemset(p->d_kv_lo, 0, (size_t)c.n_seq * 4) != hipSuccess)
+        return fail(SFA_ERR_RUNTIME);
+
+    p->descs.resize(c.n_layer);
+    for (int l = 0; l < c.n_layer; ++l) {
+        sfa_kv_desc &L = p->descs[l];
+        L = d;
+        L.k_pages = p->dev_pool + (size_t)(2 * l) * c.n_pages * p->page_bytes;
+        L.v_pages = p->dev_pool + (size_t)(2 * l + 1) * c.n_pages * p->page_bytes;
+        L.n_cold_pages = c.n_cold_pages;
+        if (c.n_cold_pages > 0) {
+            L.k_cold = p->cold_pool + (size_t)(2 * l) * c.n_cold_pages * p->page_bytes;
+            L.v_cold = p->cold_pool + (size_t)(2 * l + 1) * c.n_cold_pages * p->page_bytes;
+        }
+    }
+    p->ws_bytes = sfa_decode_workspace_bytes(&p->descs[0], c.n_seq, p->max_span);
+    if (p->ws_bytes == 0) return fail(SFA_ERR_INVALID_ARGUMENT);
+    if (hipMalloc(&p->ws, p->ws_bytes) != hipSuccess) return fail(SFA_ERR_OUT_OF_MEMORY);
+    if (sfa_workspace_init(p->ws, p->ws_bytes, nullptr) != SFA_OK) return fail(SFA_ERR_RUNTIME);
+    if (hipDeviceSynchronize() != hipSuccess) return fail(SFA_ERR_RUNTIME);
+    *out = p;
+    return SFA_OK;
+}
+
+SFA_API void sfa_pager_destroy(sfa_pager *p) {
+    if (p == nullptr) return;
+    (void)hipDeviceSynchronize();  // no copy or kernel may still use the pools
+    delete p;
+}
+
+SFA_API int sfa_pager_begin(sfa_pager *p, const int32_t *n_tok, void *stream) {
+    if (p == nullptr || n_tok == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+    const int n_seq = p->cfg.n_seq;
+    for (int b = 0; b < n_seq; ++b)
+        if (n_tok[b] < 0 || n_tok[b] > p->cfg.page_size) return SFA_ERR_INVALID_ARGUMENT;
+    std::vector<sfa::PageAction> actions;
+    try {
+        const sfa::PagePlanner saved = p->planner;
+        int32_t off = 0;
+        for (int b = 0; b < n_seq; ++b) {
+            p->step_pos0[b] = (int32_t)p->planner.store(b).used();
+            p->step_off[b] = off;
+            p->step_ntok[b] = n_tok[b];
+            off += n_tok[b];
+            if (int rc = p->planner.plan(b, n_tok[b], &actions); rc != SFA_OK) {
+                p->planner = saved;
+                p->step_open = false;
+                return rc;
+            }
+        }
+        p->step_tokens = off;
+    } catch (const std::bad_alloc &) {
+        return SFA_ERR_OUT_OF_MEMORY;
+    }
+    p->step_open = true;
+    return p->apply(actions, as_stream(stream));
+}
+
+SFA_API int sfa_pager_append(sfa_pager *p, int32_t layer, const float *k, const float *v,
+                             void *stream) {
+    if (p == nullptr || !p->step_open || layer < 0 || layer >= p->cfg.n_layer)
+        return SFA_ERR_INVALID_ARGUMENT;
+    if (p->step_tokens == 0) return SFA_OK;
+    return sfa_kv_append(&p->descs[layer], k, v, p->d_tok_seq, p->d_tok_pos, p->step_tokens,
+                         p->d_table, p->max_pages, stream);
+}
+
+SFA_API int sfa_pager_attend(sfa_pager *p, int32_t layer, const float *q, float *out,
+                             void *stream) {
+    if (p == nullptr || !p->step_open || layer < 0 || layer >= p->cfg.n_layer)
+        return SFA_ERR_INVALID_ARGUMENT;
+    const sfa_kv_desc *d = &p->descs[layer];
+    const float scale = 1.0f / std::sqrt((float)p->cfg.head_dim);
+    const bool windowed = p->cfg.attend == SFA_ATTEND_WINDOW;
+    const bool one_each = std::all_of(p->step_ntok.begin(), p->step_ntok.end(),
+                                      [](int32_t n) { return n == 1; });
+    if (one_each)
+        return sfa_attn_decode(d, q, out, p->d_table, p->max_pages, p->d_seq_len,
+                               windowed ? p->d_kv_lo : nullptr, p->cfg.n_seq, p->max_span, scale,
+                               p->ws, p->ws_bytes, stream);
+    if (windowed) return SFA_ERR_UNSUPPORTED;  // per-query windows in a chunk
+    const size_t row = (size_t)p->cfg.n_head * p->cfg.head_dim;
+    for (int b = 0; b < p->cfg.n_seq; ++b) {
+        if (p->step_ntok[b] == 0) continue;
+        const size_t off = (size_t)p->step_off[b] * row;
+        const int rc = sfa_attn_prefill(d, q + off, out + off, p->d_table + (size_t)b * p->max_pages,
+                                        p->max_pages, p->step_pos0[b], p->step_ntok[b], 0, scale,
+                                        stream);
+        if (rc != SFA_OK) return rc;
+    }
+    return SFA_OK;
+}
+
+SFA_API int sfa_pager_reset(sfa_pager *p, int32_t seq, void *stream) {
+    if (p == nullptr || seq < 0 || seq >= p->cfg.n_seq) return SFA_ERR_INVALID_ARGUMENT;
+    std::vector<sfa::PageAction> actions;
+    try {
+        p->planner.reset(seq, &actions);
+    } catch (const std::bad_alloc &) {
+        return SFA_ERR_OUT_OF_MEMORY;
+    }
+    std::fill(p->step_ntok.begin(), p->step_ntok.end(), 0);
+    for (int b = 0; b < p->cfg.n_seq; ++b) p->step_pos0[b] = (int32_t)p->planner.store(b).used();
+    p->step_tokens = 0;
+    p->step_open = false;
+    // the table slots of the released pages go back to -1
+    std::vector<std::pair<int32_t, int32_t>> edits;
+    for (int lp = 0; lp < p->max_pages; ++lp) edits.emplace_back(seq * p->max_pages + lp, -1);
+    return p->launch_updates(edits, as_stream(stream));
+}
+
+SFA_API int sfa_pager_stats_get(const sfa_pager *p, sfa_pager_stats *out) {
+    if (p == nullptr || out == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+    const sfa::PlannerStats &s = p->planner.stats();
+    out->pages_allocated = s.allocated;
+    out->pages_evicted = s.evicted;
+    out->pages_dropped = s.dropped;
+    out->dev_pages_in_use = s.dev_in_use;
+    out->cold_pages_in_use = s.cold_in_use;
+    out->bytes_evicted = p->bytes_evicted;
+    return SFA_OK;
+}
+
+SFA_API int sfa_pager_desc(const sfa_pager *p, int32_t layer, sfa_kv_desc *out) {
+    if (p == nullptr || out == nullptr || layer < 0 || layer >= p->cfg.n_layer)
+        return SFA_ERR_INVALID_ARGUMENT;
+    *out = p->descs[layer];
+    return SFA_OK;
+}
+
+SFA_API int32_t sfa_pager_max_pages(const sfa_pager *p) { return p ? p->max_pages : 0; }
+
+SFA_API int sfa_pager_tables(const sfa_pager *p, int32_t *page_table, int32_t *used) {
+    if (p == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+    if (page_table) std::copy(p->planner.table().begin(), p->planner.table().end(), page_table);
+    if (used)
+        for (int b = 0; b < p->cfg.n_seq; ++b) used[b] = (int32_t)p->planner.store(b).used();
+    return SFA_OK;
+}
+
+}  // extern "C"

@@ -22,6 +22,8 @@ def _ensure_built():
     from strataflow_amd import build
     if not build.LIB.exists():
         build.build_hip()
+    if not build.HOST_LIB.exists():
+        build.build_host()
     if not (build.ORACLE_DIR / "liboracle.so").exists():
         build.build_oracle()
 
