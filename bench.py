@@ -234,6 +234,107 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int):
     }
 
 
+def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 4):
+    """KV-window decode under paging pressure: 4 sequences with 65536-token
+    histories, a 4096-position window, the device pool sized to the window
+    (4 x 17 pages per layer), pages evicted and reused by the host page
+    manager every 256 steps of a sequence.  (a) the opt-in sliding window over
+    all 32 layers for `steps` decode steps; (b) the reference's lossless
+    semantics (every position attended, the 61440 evicted positions read from
+    the host-pinned cold pool in place) on one layer."""
+    from strataflow_amd import synth
+    from strataflow_amd.pager import SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, KvPager
+    dev = torch.device("cuda:0")
+    B, hist, W = 4, 65536, 4096
+    res = {}
+    for name, attend, n_layer, n_steps in (("sliding_window", SFA_ATTEND_WINDOW, N_LAYER, steps),
+                                           ("lossless", SFA_ATTEND_LOSSLESS, 1, lossless_steps)):
+        pager = KvPager(n_layer=n_layer, n_head=HQ, n_head_kv=HKV, head_dim=HD, kv_type=SFA_KV_F16,
+                        page_size=PAGE, n_seq=B, n_ctx=hist + n_steps, window=W, attend=attend,
+                        seed=seed)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        for c0 in range(0, hist, PAGE):
+            assert pager.begin(np.full(B, PAGE, np.int32)) == 0
+            pos = (c0 + torch.arange(PAGE, device=dev, dtype=torch.int32)).repeat(B)
+            for layer in range(n_layer):
+                k = synth.rope_normal_torch(torch.randn((B * PAGE, HKV, HD), device=dev, generator=gen),
+                                            pos, 1e6).contiguous()
+                v = torch.randn((B * PAGE, HKV, HD), device=dev, generator=gen)
+                pager.append(layer, k, v)
+        pos = torch.arange(hist, hist + n_steps, device=dev, dtype=torch.int32)
+        qs = synth.rope_normal_torch(
+            torch.randn((n_steps * n_layer * B, HQ, HD), device=dev, generator=gen),
+            pos.repeat_interleave(n_layer * B), 1e6).view(n_steps, n_layer, B, HQ, HD).contiguous()
+        ks = synth.rope_normal_torch(
+            torch.randn((n_steps * n_layer * B, HKV, HD), device=dev, generator=gen),
+            pos.repeat_interleave(n_layer * B), 1e6).view(n_steps, n_layer, B, HKV, HD).contiguous()
+        vs = torch.randn((n_steps, n_layer, B, HKV, HD), device=dev, generator=gen)
+        out = torch.empty((n_layer, B, HQ * HD), device=dev)
+        ones = np.ones(B, np.int32)
+        # a decode step's per-layer calls take the same arguments every step
+        # (the pager's device tables change, not their addresses), so the
+        # layer loop is one HIP graph over fixed input buffers; each step is
+        # the pager's host planning + table-update kernel, the copy of that
+        # step's Q/K/V into the buffers, and a replay
+        qb, kb, vb = qs[0].clone(), ks[0].clone(), vs[0].clone()
+
+        def layers():
+            for layer in range(n_layer):
+                pager.append(layer, kb[layer], vb[layer])
+                pager.attend(layer, qb[layer], out[layer])
+
+        assert pager.begin(ones) == 0  # one warm step (not timed) opens a step
+        layers()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            layers()
+        # the capture recorded but did not run the warm step's calls again;
+        # the pager is one position ahead of the histories from here on
+        torch.cuda.synchronize()
+        calibrate_backlog(torch)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gpu_backlog(torch, 20)
+        t0.record()
+        for s in range(n_steps - 1):
+            assert pager.begin(ones) == 0
+            qb.copy_(qs[s + 1])
+            kb.copy_(ks[s + 1])
+            vb.copy_(vs[s + 1])
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        n_steps -= 1
+        us = t0.elapsed_time(t1) * 1e3 / (n_steps * n_layer)
+        st = pager.stats()
+        hbm = B * W * HKV * HD * 2 * 2
+        entry = {
+            "workload": f"decode-attn f16 KV, Mixtral GQA 32q/8kv hd128, B={B}, history {hist}, "
+                        f"window {W}, device pool {B * (W // PAGE + 1)} pages/layer, "
+                        f"{n_steps} consecutive steps, {n_layer} layer(s)",
+            "semantics": ("sliding window: attends the last 4096 positions (opt-in kv_lo)"
+                          if attend == SFA_ATTEND_WINDOW else
+                          "lossless (reference): attends every position; evicted pages read "
+                          "from the host-pinned cold pool"),
+            "us_per_layer_step": round(us, 3),
+            "us_per_layer_token": round(us / B, 3),
+            "includes": "paging (plan + table update), KV append, split-K decode and merge",
+            "pages_evicted": st["pages_evicted"], "pages_dropped": st["pages_dropped"],
+            "hbm_bytes_per_layer_step": hbm,
+            "hbm_gbs": round(hbm / (us * 1e-6) / 1e9, 1),
+        }
+        if attend == SFA_ATTEND_LOSSLESS:
+            cold = sum(hist + s - W for s in range(n_steps)) // n_steps * B * HKV * HD * 2 * 2
+            entry["host_link_bytes_per_layer_step"] = cold
+            entry["host_link_gbs"] = round(cold / (us * 1e-6) / 1e9, 1)
+        res[name] = entry
+        pager.close()
+        del qs, ks, vs
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(kv, pt, q_layer0, ctx, budget_s=12.0):
     """The oracle (ggml semantics, the reference's op sequence with its three
     history copies) on the host cores, layer 0 of the same workload."""
@@ -268,6 +369,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 decode legs")
+    ap.add_argument("--no-window", action="store_true", help="skip the KV-window paging legs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
     args = ap.parse_args()
@@ -336,6 +438,8 @@ def main():
         result["prefill"] = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1)
     if not args.no_q8:
         result["q8_0"] = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2)
+    if not args.no_window:
+        result["window"] = window_bench(torch, args.seed + 3)
     if not args.no_cpu:
         threads, res = cpu_baseline(kv, pt, q[0], ctx)
         us_all, n_all, cpu_out = res[threads]
