@@ -116,3 +116,25 @@ class Case:
                               kv_lo=self.t_lo, **kw)
         torch.cuda.synchronize()
         return out.cpu().numpy()
+
+
+class OracleAttention:
+    """The attention node on the CPU oracle, with the call shape of
+    strataflow_amd.tiny_moe.HipAttention: per layer a host paged f16 cache,
+    append at pos0.., attention of the T new tokens (causal)."""
+
+    def __init__(self, oracle_mod, cfg, n_ctx: int, mode: int):
+        self.o, self.cfg, self.mode = oracle_mod, cfg, mode
+        n_pages = (n_ctx + cfg.page_size - 1) // cfg.page_size
+        self.pt = np.arange(n_pages, dtype=np.int32)[None]
+        self.host = [oracle_mod.HostPagedKv(cfg.n_head_kv, cfg.head_dim, cfg.page_size,
+                                            oracle_mod.KV_F16, n_pages) for _ in range(cfg.n_layer)]
+
+    def __call__(self, layer, q, k, v, pos0):
+        T = q.shape[0]
+        pos = np.arange(pos0, pos0 + T, dtype=np.int32)
+        h = self.host[layer]
+        assert h.append(k, v, np.zeros(T, np.int32), pos, self.pt) == 0
+        out = h.attention(np.ascontiguousarray(q, np.float32)[None], self.cfg.n_head, self.pt,
+                          np.array([pos0 + T], np.int32), T=T, mode=self.mode)
+        return out.reshape(T, -1)
