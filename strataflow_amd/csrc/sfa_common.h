@@ -71,6 +71,24 @@ __device__ inline uint32_t load4_a4(const uint8_t *p) {
     return *reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
 }
 
+// Page ids of 64 consecutive logical pages of one sequence, one per lane, so
+// that a tile's page id is a v_readlane instead of a dependent memory load on
+// every tile (a wave's tiles rarely leave one window; when they do, the
+// window moves).  `lp` must be wave-uniform.
+struct PageWindow {
+    int base;
+    int32_t ids;
+    __device__ inline void load(const int32_t *pt, int max_pages, int first, int lane) {
+        base = first;
+        const int lp = first + lane;
+        ids = lp < max_pages ? pt[lp] : -1;
+    }
+    __device__ inline int32_t get(const int32_t *pt, int max_pages, int lp, int lane) {
+        if (lp < base || lp >= base + kWave) load(pt, max_pages, lp, lane);
+        return __builtin_amdgcn_readlane(ids, lp - base);
+    }
+};
+
 // Cross-half exchange: value of lane (l ^ 32).
 __device__ inline float xor32(float x) {
     return __shfl_xor(x, 32, 64);

@@ -91,12 +91,12 @@ __device__ inline bool split_coords(const DecodeParams &p, int &split, int &kvh,
 
 // Active tile range of sequence b: tiles are 32-aligned absolute position
 // blocks [32t, 32t+32) intersecting [lo, n_kv).
-__device__ inline void seq_tiles(const DecodeParams &p, int b, int &lo, int &n_kv, int &t0,
-                                 int &n_tiles, int &tps, int &n_active) {
-    n_kv = p.seq_len[b];
+__device__ inline void seq_tiles_from(const DecodeParams &p, int n_kv_raw, int lo_raw, int &lo,
+                                      int &n_kv, int &t0, int &n_tiles, int &tps, int &n_active) {
+    n_kv = n_kv_raw;
     const int cap = p.max_pages * p.page_size;
     if (n_kv > cap) n_kv = cap;
-    lo = p.kv_lo ? p.kv_lo[b] : 0;
+    lo = lo_raw;
     if (lo < 0) lo = 0;
     if (n_kv <= lo) {
         t0 = 0; n_tiles = 0; tps = 1; n_active = 0;
@@ -108,6 +108,10 @@ __device__ inline void seq_tiles(const DecodeParams &p, int b, int &lo, int &n_k
     const int need = (n_tiles + p.n_splits - 1) / p.n_splits;
     if (tps < need) tps = need;
     n_active = (n_tiles + tps - 1) / tps;
+}
+__device__ inline void seq_tiles(const DecodeParams &p, int b, int &lo, int &n_kv, int &t0,
+                                 int &n_tiles, int &tps, int &n_active) {
+    seq_tiles_from(p, p.seq_len[b], p.kv_lo ? p.kv_lo[b] : 0, lo, n_kv, t0, n_tiles, tps, n_active);
 }
 
 // Workgroup epilogue of a split: the four waves' (m, l, O^T) for the g heads
@@ -199,11 +203,12 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     // Returns false (wave-uniform) when the tile's page id is invalid.
     half8 kf[KC];
     half8 vr[VIT];
+    PageWindow pages;
     auto issue = [&](int t) -> bool {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
         if (lpage >= p.max_pages) return false;
-        const int32_t pid = __builtin_amdgcn_readfirstlane(pt[lpage]);
+        const int32_t pid = pages.get(pt, p.max_pages, lpage, lane);
         const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
         const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
         if (kb == nullptr || vb == nullptr) return false;
@@ -219,14 +224,39 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
         return true;
     };
 
-    // The first tile as the host plan places it (kv_lo 0, seq_len within the
-    // plan) is fetched before seq_len is known; re-issued below if the guess
-    // was wrong.
+    // Prologue order matters: loads complete in issue order (one vmcnt), so
+    // the small loads a wave waits on first (its page-id window, seq_len /
+    // kv_lo, its Q chunk) are issued before the first tile's K/V burst; the
+    // first tile, as the host plan places it (kv_lo 0, seq_len within the
+    // plan), is fetched before seq_len is known and re-issued below if the
+    // guess was wrong.
     const int t_guess = __builtin_amdgcn_readfirstlane(split * p.tiles_per_split + wave);
+    pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
+    const int n_kv_raw = p.seq_len[b];
+    const int lo_raw = p.kv_lo ? p.kv_lo[b] : 0;
+    // Q of the g heads rounded to f16 (the F16 vec_dot_type conversion ggml
+    // applies to src1), staged once per workgroup in LDS; the Q^T operand of
+    // column n (head n % g, dims 16c + 8hh .. +8) is re-read per tile, which
+    // keeps 32 registers free.  One 8-element chunk per thread.
+    static_assert(G * HD / 8 <= 256, "one Q chunk per thread");
+    const bool q_thread = threadIdx.x < G * HD / 8;
+    floatx4 qx0 = floatx4{}, qx1 = floatx4{};
+    if (q_thread) {
+        const floatx4 *qr = reinterpret_cast<const floatx4 *>(
+            p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD);
+        qx0 = qr[2 * threadIdx.x];
+        qx1 = qr[2 * threadIdx.x + 1];
+    }
     bool tile_ok = issue(t_guess);
+    if (q_thread) {
+        half8 h;
+        h[0] = (_Float16)qx0[0]; h[1] = (_Float16)qx0[1]; h[2] = (_Float16)qx0[2]; h[3] = (_Float16)qx0[3];
+        h[4] = (_Float16)qx1[0]; h[5] = (_Float16)qx1[1]; h[6] = (_Float16)qx1[2]; h[7] = (_Float16)qx1[3];
+        reinterpret_cast<half8 *>(lds_q)[threadIdx.x] = h;
+    }
 
     int lo, n_kv, t0, n_tiles, tps, n_active;
-    seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
+    seq_tiles_from(p, n_kv_raw, lo_raw, lo, n_kv, t0, n_tiles, tps, n_active);
     float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
     if (split >= n_active) {
         if (split == 0 && n_active == 0) {
@@ -239,23 +269,6 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
     int t = tile_lo + wave_u;
     if (t != t_guess) tile_ok = t < tile_hi ? issue(t) : false;
-
-    // Q of the g heads rounded to f16 (the F16 vec_dot_type conversion ggml
-    // applies to src1), staged once per workgroup in LDS; the Q^T operand of
-    // column n (head n % g, dims 16c + 8hh .. +8) is re-read per tile, which
-    // keeps 32 registers free.  Loaded after the first tile's K/V so both
-    // latencies overlap.
-    {
-        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
-        for (int i = threadIdx.x; i < G * HD / 8; i += blockDim.x) {
-            const floatx4 x0 = reinterpret_cast<const floatx4 *>(qr)[2 * i];
-            const floatx4 x1 = reinterpret_cast<const floatx4 *>(qr)[2 * i + 1];
-            half8 h;
-            h[0] = (_Float16)x0[0]; h[1] = (_Float16)x0[1]; h[2] = (_Float16)x0[2]; h[3] = (_Float16)x0[3];
-            h[4] = (_Float16)x1[0]; h[5] = (_Float16)x1[1]; h[6] = (_Float16)x1[2]; h[7] = (_Float16)x1[3];
-            reinterpret_cast<half8 *>(lds_q)[i] = h;
-        }
-    }
     __syncthreads();
     const half8 *qrow = reinterpret_cast<const half8 *>(lds_q) + (n % G) * (HD / 8) + hh;
 
@@ -419,11 +432,12 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     intx4 kq[NB];
     uint32_t kd[NB];             // dword holding d_k of block c
     uint32_t vw[VBL][9];         // the 36 bytes around each V block
+    PageWindow pages;
     auto issue = [&](int t) -> bool {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
         if (lpage >= p.max_pages) return false;
-        const int32_t pid = __builtin_amdgcn_readfirstlane(pt[lpage]);
+        const int32_t pid = pages.get(pt, p.max_pages, lpage, lane);
         const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
         const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
         if (kb == nullptr || vb == nullptr) return false;
@@ -463,22 +477,34 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
         return true;
     };
 
+    // Prologue order as in the f16 kernel: page-id window, seq_len / kv_lo
+    // and the lane's Q values are issued before the first tile's K/V burst.
     const int t_guess = __builtin_amdgcn_readfirstlane(split * p.tiles_per_split + wave);
+    pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
+    const int n_kv_raw = p.seq_len[b];
+    const int lo_raw = p.kv_lo ? p.kv_lo[b] : 0;
+    const int hq = n % G;
+    floatx4 qraw[NB][4];
+    {
+        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G + hq) * HD;
+#pragma unroll
+        for (int c = 0; c < NB; ++c)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                qraw[c][j] = reinterpret_cast<const floatx4 *>(qr + 32 * c + 16 * hh)[j];
+    }
     bool tile_ok = issue(t_guess);
 
     // Q8_0 of Q, the MFMA A operand: lane row m = n is head n % G, block c,
     // elements 16hh .. 16hh+15.
-    const int hq = n % G;
     intx4 qa[NB];
     {
-        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G + hq) * HD;
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
             float x[16];
-            const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 32 * c + 16 * hh);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const floatx4 v4 = src[j];
+                const floatx4 v4 = qraw[c][j];
                 x[4 * j] = v4[0]; x[4 * j + 1] = v4[1]; x[4 * j + 2] = v4[2]; x[4 * j + 3] = v4[3];
             }
             float amax = 0.0f;
@@ -498,7 +524,7 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     }
 
     int lo, n_kv, t0, n_tiles, tps, n_active;
-    seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
+    seq_tiles_from(p, n_kv_raw, lo_raw, lo, n_kv, t0, n_tiles, tps, n_active);
     float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
     if (split >= n_active) {
         if (split == 0 && n_active == 0) {
@@ -695,52 +721,68 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
 }
 
 // Second pass: out = sum_s o_s * 2^(m_s - M) / sum_s l_s * 2^(m_s - M) over
-// the active splits of each (sequence, kv head), in split order.  One
-// workgroup per (b, kv head, group head), one thread per dim.
+// the active splits of each (sequence, kv head), in split order, 64 splits per
+// round.  One workgroup per (b, kv head, group head), one thread per dim; the
+// (m, l) of the round's splits are loaded one split per lane and broadcast
+// with v_readlane.  The first round's loads are issued before seq_len is
+// read (the workspace holds n_splits records whatever the lengths), so the
+// kernel waits on memory once.
 template <int HD, int G>
 __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeParams p) {
-    constexpr int CH = 32;  // splits whose loads are in flight together
+    constexpr int CH = kWave;
     const int g = blockIdx.x % G;
     const int kvh = (blockIdx.x / G) % p.n_head_kv;
     const int b = blockIdx.x / (G * p.n_head_kv);
     const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int d = tid < HD ? tid : HD - 1;  // threads past HD (HD < 64) only load (m, l)
+    const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
+    const float *pg = p.part + head_base * p.n_splits * G * (HD + 4) + g * (HD + 4);
+    const int64_t sstride = (int64_t)G * (HD + 4);
+    const int S = p.n_splits;
+
+    float o[CH], mv, lv;
+    auto load_round = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < CH; ++u) o[u] = s0 + u < S ? pg[(s0 + u) * sstride + d] : 0.0f;
+        const int sl = s0 + lane;
+        mv = sl < S ? pg[sl * sstride + HD] : -INFINITY;
+        lv = sl < S ? pg[sl * sstride + HD + 1] : 0.0f;
+    };
+    auto bcast = [](float x, int u) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), u));
+    };
+    load_round(0);
     int lo, n_kv, t0, n_tiles, tps, n_active;
     seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
-    if (n_active <= 1 || tid >= HD) return;  // one split: written by the split pass
-    const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
-    const float *pbase = p.part + head_base * p.n_splits * G * (HD + 4) + g * (HD + 4);
-    const int64_t sstride = (int64_t)G * (HD + 4);
-    // log-sum-exp merge in split order, CH splits per round: every load of a
-    // round is issued before any is used
+    if (n_active <= 1) return;  // one split: written by the split pass
+
     float M = -INFINITY, L = 0.0f, O = 0.0f;
     for (int s0 = 0; s0 < n_active; s0 += CH) {
-        float m[CH], l[CH], o[CH];
-#pragma unroll
-        for (int u = 0; u < CH; ++u) {
-            const int s = s0 + u < n_active ? s0 + u : n_active - 1;
-            const float *ps = pbase + s * sstride;
-            m[u] = ps[HD];
-            l[u] = ps[HD + 1];
-            o[u] = ps[tid];
-        }
+        if (s0 > 0) load_round(s0);
         float mc = M;
 #pragma unroll
         for (int u = 0; u < CH; ++u)
-            if (s0 + u < n_active) mc = fmaxf(mc, m[u]);
+            if (s0 + u < n_active) mc = fmaxf(mc, bcast(mv, u));
         if (mc == -INFINITY) continue;
         const float a = __builtin_amdgcn_exp2f(M - mc);  // M == -inf -> 0
         L *= a;
         O *= a;
 #pragma unroll
         for (int u = 0; u < CH; ++u) {
-            const float w = (s0 + u < n_active && m[u] != -INFINITY) ? __builtin_amdgcn_exp2f(m[u] - mc) : 0.0f;
-            L += l[u] * w;
-            O += o[u] * w;
+            if (s0 + u < n_active) {
+                const float m = bcast(mv, u);
+                const float wt = m != -INFINITY ? __builtin_amdgcn_exp2f(m - mc) : 0.0f;
+                L += bcast(lv, u) * wt;
+                O += o[u] * wt;
+            }
         }
         M = mc;
     }
-    float *out = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD;
-    out[tid] = L > 0.0f ? O / L : 0.0f;
+    if (tid < HD) {
+        float *out = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD;
+        out[tid] = L > 0.0f ? O / L : 0.0f;
+    }
 }
 
 // ---- host side -------------------------------------------------------------
