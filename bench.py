@@ -17,6 +17,7 @@ Prints ONE JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -89,11 +90,15 @@ def calibrate_backlog(torch) -> None:
     gpu_backlog.cycles_per_s = 1_000_000 / max(a.elapsed_time(b) * 1e-3, 1e-6)
 
 
+def _lib_mod():
+    from strataflow_amd import _lib
+    return _lib
+
+
 def time_decode(torch, kv, t_pt, q, seq_len, ctx, steps, warmup):
     """Step timing: the 32-layer loop captured once as a HIP graph and
-    replayed `steps` times between two events.  Kernel timing: events around
-    every split-K launch of the same loop, queued behind a backlog so the
-    launches run back to back."""
+    replayed `steps` times between two events.  Kernel timing: the split-K
+    passes of the 32 layers back to back between two events."""
     B = int(seq_len.numel())
     out = torch.empty((N_LAYER, B, HQ * HD), device=q.device)
     kv.workspace(B, ctx)
@@ -127,51 +132,110 @@ def time_decode(torch, kv, t_pt, q, seq_len, ctx, steps, warmup):
     torch.cuda.synchronize()
     ms_eager = t0.elapsed_time(t1) / steps
 
+    # split-K kernel time: the split passes of all layers back to back between
+    # two events (queued behind a backlog, so host launch cost is hidden),
+    # divided by the launch count; repeated `steps` times
     calibrate_backlog(torch)
+    lib = _lib_mod().load()
+    ws = kv.workspace(B, ctx)
+    stream = torch.cuda.current_stream().cuda_stream
+    args = [(ctypes.byref(kv.desc(layer)), q[layer].data_ptr(), out[layer].data_ptr(), t_pt.data_ptr(),
+             int(t_pt.shape[1]), seq_len.data_ptr(), None, B, int(ctx), float(kv.scale), ws.data_ptr(),
+             ws.numel(), stream) for layer in range(N_LAYER)]
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(N_LAYER * steps)]
+           for _ in range(steps)]
     torch.cuda.synchronize()
     gpu_backlog(torch, 0.05 * N_LAYER * steps + 5)
-    i = 0
-    for _ in range(steps):
+    for a, b in evs:
+        a.record()
         for layer in range(N_LAYER):
-            evs[i][0].record()
-            kv.decode(layer, q[layer], t_pt, seq_len, ctx, out=out[layer], split_end_event=evs[i][1])
-            i += 1
+            lib.sfa_attn_decode_split(*args[layer])
+        b.record()
     torch.cuda.synchronize()
-    durs = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3  # us
+    durs = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3 / N_LAYER  # us per launch
+    for layer in range(N_LAYER):  # leave complete outputs behind
+        kv.decode(layer, q[layer], t_pt, seq_len, ctx, out=out[layer])
+    torch.cuda.synchronize()
     return ms_per_step, ms_eager, float(np.mean(durs)), float(np.median(durs)), out
+
+
+def load_traffic() -> dict:
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE (scaled by a plain copy's readings), recorded per workload in
+    profiles/traffic.json by the profiling runs quoted in profiles/*.txt."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
+def with_traffic(roofline: dict, key: str) -> dict:
+    t = load_traffic().get(key)
+    if t:
+        roofline["traffic"] = t["bytes_per_launch"]
+        roofline["traffic_source"] = f"profiles/traffic.json[{key}] (rocprofv3 FETCH_SIZE+WRITE_SIZE)"
+    return roofline
+
+
+def decode_leg(torch, key, lens, kv_type, steps, warmup, seed):
+    """One decode workload: lens (one entry per sequence), f16 or Q8_0."""
+    kv, pt, t_pt, q, seq_len = build_decode_workload(torch, lens, seed, kv_type=kv_type)
+    mx = int(max(lens))
+    ms, _, k_mean, _, _ = time_decode(torch, kv, t_pt, q, seq_len, mx, steps, warmup)
+    row = HD * 2 if kv_type == 1 else HD // 32 * 34
+    alg = 2 * sum(lens) * HKV * row + len(lens) * HQ * HD * 4 * 2
+    us_layer = ms * 1e3 / N_LAYER
+    ach = alg / (k_mean * 1e-6) / 1e9
+    kname = "decode_f16_kernel<128,4>" if kv_type == 1 else "decode_q8_kernel<128,4>"
+    res = {
+        "workload": f"decode-attn {'f16' if kv_type == 1 else 'Q8_0'} KV, Mixtral GQA 32q/8kv hd128, "
+                    f"B={len(lens)}, context {lens if len(lens) > 1 else lens[0]}, 256-token pages "
+                    f"shuffled, {N_LAYER} layers with distinct caches",
+        "us_per_layer_step": round(us_layer, 3),
+        "us_per_layer_token": round(us_layer / len(lens), 3),
+        "tokens_per_s": round(len(lens) * 1e3 / ms, 1),
+        "roofline": with_traffic({
+            "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": f"{kname} (split-K pass)", "kernel_us_mean": round(k_mean, 3),
+            "bytes_per_launch": alg}, key),
+    }
+    del kv, q
+    torch.cuda.empty_cache()
+    return res
 
 
 def q8_bench(torch, steps, warmup, seed):
     """Q8_0 KV decode: (a) batch 1 at context 32768; (b) batch 8 with lengths
     uniform in [8192, 32768] sharing one page pool."""
-    res = {}
-    row_q8 = HD // 32 * 34
-    for name, lens in (("ctx32k_b1", [32768]),
-                       ("b8_varlen_8k_32k", [int(x) for x in np.random.default_rng(seed).integers(8192, 32769, 8)])):
-        kv, pt, t_pt, q, seq_len = build_decode_workload(torch, lens, seed, kv_type=8)
-        mx = int(max(lens))
-        ms, ms_eager, k_mean, k_med, _ = time_decode(torch, kv, t_pt, q, seq_len, mx, steps, warmup)
-        kv_bytes = 2 * sum(lens) * HKV * row_q8
-        alg = kv_bytes + len(lens) * HQ * HD * 4 * 2
-        us_layer = ms * 1e3 / N_LAYER
-        ach = alg / (k_mean * 1e-6) / 1e9
-        res[name] = {
-            "workload": f"decode-attn Q8_0 KV, Mixtral GQA 32q/8kv hd128, B={len(lens)}, "
-                        f"context {lens if len(lens) > 1 else lens[0]}, 256-token pages shuffled, "
-                        f"{N_LAYER} layers",
-            "us_per_layer_step": round(us_layer, 3),
-            "us_per_layer_token": round(us_layer / len(lens), 3),
-            "tokens_per_s": round(len(lens) * 1e3 / ms, 1),
-            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": "decode_q8_kernel<128,4> (split-K pass)",
-                         "kernel_us_mean": round(k_mean, 3), "bytes_per_launch": alg},
-        }
-        del kv, q
-        torch.cuda.empty_cache()
-    return res
+    lens_b8 = [int(x) for x in np.random.default_rng(seed).integers(8192, 32769, 8)]
+    return {
+        "ctx32k_b1": decode_leg(torch, "decode_q8_0_ctx32k_b1", [32768], 8, steps, warmup, seed),
+        "b8_varlen_8k_32k": decode_leg(torch, "decode_q8_0_b8", lens_b8, 8, steps, warmup, seed),
+    }
+
+
+def copy_ceiling(torch) -> dict:
+    """A plain 2 GiB device-to-device copy (read + write): the practical HBM
+    rate on this part, next to the nominal peak."""
+    n = 2 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(5):
+        b.copy_(a)
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / 5
+    del a, b
+    torch.cuda.empty_cache()
+    return {"bytes": 2 * n, "us": round(us, 1), "gbs": round(2 * n / us / 1e3, 1),
+            "what": "2 GiB device copy (read + write bytes), torch"}
 
 
 def prefill_bench(torch, steps: int, warmup: int, seed: int):
@@ -227,9 +291,10 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int):
         "us_per_layer_chunk": round(us, 2),
         "us_per_layer_token": round(us / T, 5),
         "tflops": round(tflops, 1),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                     "traffic": None},
+        "roofline": with_traffic({"bound": "mfma", "achieved": round(tflops, 1),
+                                  "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                                  "kernel": "prefill_f16_kernel<128,4>"}, "prefill_2048_on_2048"),
         "flop_per_layer_chunk": flops,
     }
 
@@ -370,6 +435,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 decode legs")
     ap.add_argument("--no-window", action="store_true", help="skip the KV-window paging legs")
+    ap.add_argument("--no-32k", action="store_true", help="skip the f16 context-32768 decode leg")
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window"],
+                    help="run one leg only and print its JSON (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
     args = ap.parse_args()
@@ -394,6 +462,20 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": n, "reps": 5}))
+        return
+
+    if args.only == "decode4k":
+        args.no_prefill = args.no_q8 = args.no_window = args.no_32k = args.no_cpu = True
+    if args.only and args.only != "decode4k":
+        if args.only == "decode32k":
+            r = decode_leg(torch, "decode_f16_ctx32k", [32768], 1, max(args.steps // 4, 5), 3, args.seed + 4)
+        elif args.only == "q8":
+            r = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2)
+        elif args.only == "prefill":
+            r = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1)
+        else:
+            r = window_bench(torch, args.seed + 3)
+        print(json.dumps({args.only: r}))
         return
 
     ctx = args.ctx
@@ -427,19 +509,23 @@ def main():
         "timing": "32-layer step captured as a HIP graph, replayed; eager (per-call host "
                   "launch) step also reported",
         "ms_per_step_eager": round(ms_eager, 4),
-        "roofline": {
+        "roofline": with_traffic({
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "decode_f16_kernel<128,4> (split-K pass)", "kernel_us_mean": round(k_mean, 3),
             "kernel_us_median": round(k_med, 3), "bytes_per_launch": alg_bytes,
-        },
+        }, "decode_f16_ctx4096"),
     }
+    if not args.no_32k:
+        result["f16_ctx32k"] = decode_leg(torch, "decode_f16_ctx32k", [32768], 1,
+                                          max(args.steps // 4, 5), 3, args.seed + 4)
     if not args.no_prefill:
         result["prefill"] = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1)
     if not args.no_q8:
         result["q8_0"] = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2)
     if not args.no_window:
         result["window"] = window_bench(torch, args.seed + 3)
+    result["hbm_copy_ceiling"] = copy_ceiling(torch)
     if not args.no_cpu:
         threads, res = cpu_baseline(kv, pt, q[0], ctx)
         us_all, n_all, cpu_out = res[threads]
