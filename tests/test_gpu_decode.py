@@ -64,6 +64,19 @@ def test_decode_batch_varlen_window(gpu, oracle_mod):
     assert np.all(out[4] == 0)
 
 
+@pytest.mark.parametrize("kv_type,page_size", [(1, 32), (1, 512), (8, 32), (8, 512)])
+def test_decode_page_sizes_varlen(gpu, oracle_mod, kv_type, page_size):
+    # smallest and a large page size, a batch with an empty sequence, a
+    # one-token sequence and sliding-window starts inside a page
+    seq = [0, 1, 2500, 777, 64]
+    lo = [0, 0, 1999, 13, 32]
+    c = Case(oracle_mod, seq_lens=seq, kv_lo=lo, kv_type=kv_type, page_size=page_size,
+             seed=page_size + kv_type)
+    out = c.decode(max_seq_len=2500)
+    assert_close(out, c.oracle(oracle_mod.GGML), what=f"type {kv_type} page {page_size}")
+    assert np.all(out[0] == 0)
+
+
 def test_decode_page_placement_bit_identical(gpu, oracle_mod):
     # paged == contiguous, bit for bit (the reference's test_kv_paging.cpp:243
     # invariant): same logical cache, different physical page orders

@@ -63,10 +63,10 @@ def test_prefill_golden(gpu, oracle_mod):
     ((32, 8, 128), 200, 150, 120),
     ((8, 1, 128), 10, 33, 0),
 ])
-def test_prefill_vs_oracle(gpu, oracle_mod, shape, n_cached, T, kv_lo):
+def test_prefill_vs_oracle(gpu, oracle_mod, shape, n_cached, T, kv_lo, page_size=256):
     Hq, Hkv, hd = shape
     host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=Hq, Hkv=Hkv, hd=hd, n_cached=n_cached, T=T,
-                                   seed=T + hd)
+                                   page_size=page_size, seed=T + hd)
     out = run(dev, gpu, pt, q, n_cached, kv_lo)
     ref = host.attention(q[None], Hq, pt, np.array([n_kv], np.int32), np.array([kv_lo], np.int32),
                          T=T, mode=oracle_mod.GGML)[0].reshape(T, -1)
@@ -91,3 +91,38 @@ def test_prefill_mixtral_chunk_2048_on_2048(gpu, oracle_mod):
                              mode=oracle_mod.GGML)[0].reshape(-1)
         assert_close(out[t], ref, what=f"row {t}")
     assert np.all(np.isfinite(out))
+
+
+@pytest.mark.parametrize("shape,n_cached,T,kv_lo,page_size", [
+    ((16, 8, 64), 333, 97, 77, 128),     # unaligned window start, 128-position pages
+    ((32, 8, 128), 1000, 300, 0, 64),    # smallest page the prefill tiles allow
+    ((32, 4, 128), 129, 260, 0, 512),    # g = 8, 512-position pages
+    ((4, 4, 32), 0, 1, 0, 64),           # one token, no history
+])
+def test_prefill_pages_and_windows(gpu, oracle_mod, shape, n_cached, T, kv_lo, page_size):
+    test_prefill_vs_oracle(gpu, oracle_mod, shape, n_cached, T, kv_lo, page_size)
+
+
+def test_prefill_rejects_unsupported(gpu, oracle_mod):
+    import ctypes
+    import torch
+    from strataflow_amd import _lib
+    host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=8, Hkv=4, hd=32, n_cached=10, T=5, page_size=256)
+    lib = _lib.load()
+    d = dev.desc(0)
+    tq = torch.from_numpy(q).to(gpu)
+    out = torch.empty((5, 8 * 32), device=gpu)
+    tpt = torch.from_numpy(pt[0]).to(gpu)
+    s = torch.cuda.current_stream().cuda_stream
+    # positions past the page table
+    assert lib.sfa_attn_prefill(ctypes.byref(d), tq.data_ptr(), out.data_ptr(), tpt.data_ptr(), 1,
+                                300, 5, 0, 0.17, s) == _lib.SFA_ERR_INVALID_ARGUMENT
+    # a page size the 64-position tiles cannot cover
+    d32 = _lib.SfaKvDesc()
+    ctypes.memmove(ctypes.byref(d32), ctypes.byref(d), ctypes.sizeof(d))
+    d32.page_size = 32
+    assert lib.sfa_attn_prefill(ctypes.byref(d32), tq.data_ptr(), out.data_ptr(), tpt.data_ptr(),
+                                int(pt.shape[1]), 10, 5, 0, 0.17, s) == _lib.SFA_ERR_UNSUPPORTED
+    # T == 0 is a no-op
+    assert lib.sfa_attn_prefill(ctypes.byref(d), tq.data_ptr(), out.data_ptr(), tpt.data_ptr(),
+                                int(pt.shape[1]), 10, 0, 0, 0.17, s) == _lib.SFA_OK
