@@ -411,6 +411,7 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[kDecodeWaves][kTile * VROW];
     __shared__ __attribute__((aligned(16))) _Float16 lds_p[kDecodeWaves][G][kTile];
     __shared__ float lds_dq[G][NB];
+    __shared__ intx4 lds_qa[G][NB][2];
     __shared__ float lds_m[kDecodeWaves][G];
     __shared__ float lds_l[kDecodeWaves][G];
     __shared__ float lds_o[kDecodeWaves][G][HD];
@@ -428,12 +429,21 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
     // K operand of block c for lane (row n, half hh): quants 16hh..16hh+15 of
-    // block c and the block scale; V: blocks VBL*hh .. of row n, raw.
-    intx4 kq[NB];
-    uint32_t kd[NB];             // dword holding d_k of block c
-    uint32_t vw[VBL][9];         // the 36 bytes around each V block
+    // block c and the block scale; V: blocks VBL*hh .. of row n.  All kept
+    // as loaded (arithmetic on them at issue time would make the wave wait
+    // for the prefetched tile right where it issues it); the byte alignment
+    // of even K blocks happens when the tile is consumed.  Two such register
+    // sets (tiles A and B) alternate: the loop is unrolled by two so each set
+    // is loaded and consumed in place, never copied (a copy of a register
+    // still being loaded would wait for the load).
+    struct Raw {
+        intx4 kw[NB];                // 16 bytes at 34c + 16hh (c even) or 34c + 2 + 16hh (c odd)
+        uint32_t kx[NB / 2 > 0 ? NB / 2 : 1];  // the dword after them (even c)
+        uint32_t kd[NB];             // dword holding d_k of block c
+        uint32_t vw[VBL][9];         // the 36 bytes around each V block
+    };
     PageWindow pages;
-    auto issue = [&](int t) -> bool {
+    auto issue = [&](int t, Raw &r) -> bool {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
         if (lpage >= p.max_pages) return false;
@@ -450,18 +460,14 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
                 // block at 34c (4-aligned): quants of half hh start 2 bytes
                 // into the dword at 34c + 16hh; d is the low half at 34c
                 const uint8_t *w = kr + 34 * c + 16 * hh;
-                const intx4 x = load16_a4(w);
-                const uint32_t x4 = load4_a4(w + 16);
-                kq[c][0] = (int)__builtin_amdgcn_alignbyte((uint32_t)x[1], (uint32_t)x[0], 2);
-                kq[c][1] = (int)__builtin_amdgcn_alignbyte((uint32_t)x[2], (uint32_t)x[1], 2);
-                kq[c][2] = (int)__builtin_amdgcn_alignbyte((uint32_t)x[3], (uint32_t)x[2], 2);
-                kq[c][3] = (int)__builtin_amdgcn_alignbyte(x4, (uint32_t)x[3], 2);
-                kd[c] = load4_a4(kr + 34 * c);
+                r.kw[c] = load16_a4(w);
+                r.kx[c / 2] = load4_a4(w + 16);
+                r.kd[c] = load4_a4(kr + 34 * c);
             } else {
                 // block at 34c (2 mod 4): quants 4-aligned; d is the high half
                 // of the dword at 34c - 2
-                kq[c] = load16_a4(kr + 34 * c + 2 + 16 * hh);
-                kd[c] = load4_a4(kr + 34 * c - 2);
+                r.kw[c] = load16_a4(kr + 34 * c + 2 + 16 * hh);
+                r.kd[c] = load4_a4(kr + 34 * c - 2);
             }
         }
 #pragma unroll
@@ -471,8 +477,8 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
             const uint8_t *w = vr + 34 * c - (c & 1) * 2;
             const intx4 a0 = load16_a4(w), a1 = load16_a4(w + 16);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) { vw[u][j] = (uint32_t)a0[j]; vw[u][4 + j] = (uint32_t)a1[j]; }
-            vw[u][8] = load4_a4(w + 32);
+            for (int j = 0; j < 4; ++j) { r.vw[u][j] = (uint32_t)a0[j]; r.vw[u][4 + j] = (uint32_t)a1[j]; }
+            r.vw[u][8] = load4_a4(w + 32);
         }
         return true;
     };
@@ -493,11 +499,12 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
             for (int j = 0; j < 4; ++j)
                 qraw[c][j] = reinterpret_cast<const floatx4 *>(qr + 32 * c + 16 * hh)[j];
     }
-    bool tile_ok = issue(t_guess);
+    Raw ra, rb;
+    bool ok_a = issue(t_guess, ra);
 
     // Q8_0 of Q, the MFMA A operand: lane row m = n is head n % G, block c,
-    // elements 16hh .. 16hh+15.
-    intx4 qa[NB];
+    // elements 16hh .. 16hh+15; staged in LDS (read per tile, which keeps 16
+    // registers for the tile pipeline).
     {
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
@@ -517,7 +524,8 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
             for (int j = 0; j < 4; ++j) {
                 const int q0 = (int)roundf(x[4 * j] * id), q1 = (int)roundf(x[4 * j + 1] * id);
                 const int q2 = (int)roundf(x[4 * j + 2] * id), q3 = (int)roundf(x[4 * j + 3] * id);
-                qa[c][j] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
+                const int w4 = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
+                if (wave == 0 && n < G) lds_qa[n][c][hh][j] = w4;
             }
             if (wave == 0 && hh == 0 && n < G) lds_dq[n][c] = (float)(_Float16)d;
         }
@@ -532,19 +540,14 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
         }
         return;
     }
-    __syncthreads();  // lds_dq
-    // d_q of the heads of output rows i = 0..3 (rows 4hh + i, head (4hh+i) % G)
-    float dq[4][NB];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int c = 0; c < NB; ++c) dq[i][c] = lds_dq[(4 * hh + i) % G][c];
+    __syncthreads();  // lds_qa, lds_dq (d_q of the heads of output rows i = 0..3,
+                      // i.e. rows 4hh + i, head (4hh + i) % G, read per tile)
 
     const int tile_lo = t0 + split * tps;
     int tile_hi = tile_lo + tps;
     if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
     int t = tile_lo + wave_u;
-    if (t != t_guess) tile_ok = t < tile_hi ? issue(t) : false;
+    if (t != t_guess) ok_a = t < tile_hi ? issue(t, ra) : false;
 
     floatx16 o[DB];
 #pragma unroll
@@ -554,23 +557,32 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     for (int h = 0; h < G; ++h) { m_run[h] = -INFINITY; l_run[h] = 0.0f; alpha_h[h] = 1.0f; }
     bool first = true;
 
-    for (; t < tile_hi; t += kDecodeWaves) {
+    // part 1 of a tile: the scores and the V tile (the raw registers are dead
+    // after it); part 2: softmax and PV
+    auto consume1 = [&](int t, const Raw &r, float (&sv)[4]) {
         const int pos0 = t * kTile;
-        if (!tile_ok) {
-            tile_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
-            continue;
-        }
         const bool row_ok = pos0 + n >= lo && pos0 + n < n_kv;
         const bool interior = pos0 >= lo && pos0 + kTile <= n_kv;
         // S = Q8 * K8^T per block, scaled in block order
-        float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = 0.0f;
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
-            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[c], kq[c], intx16{}, 0, 0, 0);
-            const uint32_t dbits = (c & 1) ? (kd[c] >> 16) : (kd[c] & 0xffffu);
+            intx4 kq = r.kw[c];
+            if ((c & 1) == 0) {
+                const uint32_t *x = reinterpret_cast<const uint32_t *>(&r.kw[c]);
+                kq[0] = (int)__builtin_amdgcn_alignbyte(x[1], x[0], 2);
+                kq[1] = (int)__builtin_amdgcn_alignbyte(x[2], x[1], 2);
+                kq[2] = (int)__builtin_amdgcn_alignbyte(x[3], x[2], 2);
+                kq[3] = (int)__builtin_amdgcn_alignbyte(r.kx[c / 2], x[3], 2);
+            }
+            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lds_qa[n % G][c][hh], kq, intx16{}, 0, 0, 0);
+            const uint32_t dbits = (c & 1) ? (r.kd[c] >> 16) : (r.kd[c] & 0xffffu);
             const float dk = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sv[i] += (float)acc[i] * (dk * dq[i][c]);
+            for (int i = 0; i < 4; ++i) sv[i] += (float)acc[i] * (dk * lds_dq[(4 * hh + i) % G][c]);
+            // one block's 16-register accumulator live at a time
+            __builtin_amdgcn_sched_barrier(0);
         }
         // V blocks: dequantise into the f16 LDS tile (rows outside [lo, n_kv) zeroed)
 #pragma unroll
@@ -579,13 +591,13 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
             uint32_t q[8];
             uint32_t dbits;
             if ((c & 1) == 0) {
-                dbits = vw[u][0] & 0xffffu;
+                dbits = r.vw[u][0] & 0xffffu;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(vw[u][j + 1], vw[u][j], 2);
+                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(r.vw[u][j + 1], r.vw[u][j], 2);
             } else {
-                dbits = vw[u][0] >> 16;
+                dbits = r.vw[u][0] >> 16;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = vw[u][j + 1];
+                for (int j = 0; j < 8; ++j) q[j] = r.vw[u][j + 1];
             }
             const float dv = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
             half8 h[4];
@@ -601,7 +613,11 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
             for (int k = 0; k < 4; ++k)
                 *reinterpret_cast<half8 *>(vt + n * VROW + 64 * c + 16 * k) = h[k];
         }
-        const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
+    };
+    auto consume2 = [&](int t, float (&sv)[4]) {
+        const int pos0 = t * kTile;
+        const bool row_ok = pos0 + n >= lo && pos0 + n < n_kv;
+        const bool interior = pos0 >= lo && pos0 + kTile <= n_kv;
 
         // online softmax per head (log2 domain); this lane holds position n
         // for the heads (4hh + i) % G of registers i = 0..3 (i % G when
@@ -672,35 +688,46 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
 #pragma unroll
             for (int j = 0; j < 4; ++j) { pb[kk][j] = a0[j]; pb[kk][4 + j] = a1[j]; }
         }
-        half8 va[2][DB];
         {
             const int gq = lane >> 4, rr = lane & 15;
             const uint8_t *vsrc = vt + (4 * (gq >> 1) + (rr >> 2)) * VROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
+                half8 va[DB];
 #pragma unroll
                 for (int d = 0; d < DB; ++d) {
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
                         const half4 h = tr16_read(vsrc + (16 * kk + 8 * u) * VROW + 64 * d);
-                        va[kk][d][4 * u + 0] = h[0];
-                        va[kk][d][4 * u + 1] = h[1];
-                        va[kk][d][4 * u + 2] = h[2];
-                        va[kk][d][4 * u + 3] = h[3];
+                        va[d][4 * u + 0] = h[0];
+                        va[d][4 * u + 1] = h[1];
+                        va[d][4 * u + 2] = h[2];
+                        va[d][4 * u + 3] = h[3];
                     }
                 }
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d], pb[kk], o[d], 0, 0, 0);
             }
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-            for (int d = 0; d < DB; ++d)
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kk][d], pb[kk], o[d], 0, 0, 0);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        tile_ok = next_ok;
+    };
+
+    // tiles t (set A) and t + 4 (set B) per trip; the next tile is issued
+    // into the other set as soon as a tile's raw registers are consumed, so
+    // one tile is in flight while the current one finishes
+    float sv[4];
+    for (; t < tile_hi; t += 2 * kDecodeWaves) {
+        const int t1 = t + kDecodeWaves;
+        if (ok_a) consume1(t, ra, sv);
+        const bool ok_b = t1 < tile_hi ? issue(t1, rb) : false;
+        if (ok_a) consume2(t, sv);
+        if (t1 >= tile_hi) break;
+        if (ok_b) consume1(t1, rb, sv);
+        ok_a = t1 + kDecodeWaves < tile_hi ? issue(t1 + kDecodeWaves, ra) : false;
+        if (ok_b) consume2(t1, sv);
     }
 
     // per-head sums over all 64 lanes (each position counted once per head)
