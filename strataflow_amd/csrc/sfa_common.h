@@ -94,4 +94,32 @@ __device__ inline float xor32(float x) {
     return __shfl_xor(x, 32, 64);
 }
 
+// Value of another lane of the same 16-lane row, DPP control CTRL (all rows
+// and banks enabled, every source lane inside the row).
+template <int CTRL>
+__device__ inline float dpp_row(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+__device__ inline float lane_val(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Wave-wide max and sum (the same value in every lane): butterflies inside
+// each 16-lane row (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror), then the four row results in a fixed order.
+__device__ inline float wave_max(float x) {
+    x = fmaxf(x, dpp_row<0xB1>(x));
+    x = fmaxf(x, dpp_row<0x4E>(x));
+    x = fmaxf(x, dpp_row<0x141>(x));
+    x = fmaxf(x, dpp_row<0x140>(x));
+    return fmaxf(fmaxf(lane_val(x, 0), lane_val(x, 16)), fmaxf(lane_val(x, 32), lane_val(x, 48)));
+}
+__device__ inline float wave_sum(float x) {
+    x += dpp_row<0xB1>(x);
+    x += dpp_row<0x4E>(x);
+    x += dpp_row<0x141>(x);
+    x += dpp_row<0x140>(x);
+    return (lane_val(x, 0) + lane_val(x, 16)) + (lane_val(x, 32) + lane_val(x, 48));
+}
+
 }  // namespace sfa

@@ -53,6 +53,7 @@ struct DecodeParams {
 };
 
 constexpr int kDecodeWaves = 4;
+constexpr int kMaxSplits = 256;  // splits per (sequence, kv head)
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold: P <= 2^8
 // merge kernel block: one thread per dim, at least one full wave
 template <int HD>
@@ -748,15 +749,18 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
 }
 
 // Second pass: out = sum_s o_s * 2^(m_s - M) / sum_s l_s * 2^(m_s - M) over
-// the active splits of each (sequence, kv head), in split order, 64 splits per
-// round.  One workgroup per (b, kv head, group head), one thread per dim; the
-// (m, l) of the round's splits are loaded one split per lane and broadcast
-// with v_readlane.  The first round's loads are issued before seq_len is
-// read (the workspace holds n_splits records whatever the lengths), so the
-// kernel waits on memory once.
+// the active splits of each (sequence, kv head), M the largest m_s.  One
+// workgroup per (b, kv head, group head), one thread per dim.  Every load of
+// the first 64 splits (the lane-parallel (m, l) of all splits and this dim's
+// o_s) is issued before seq_len is read, so the kernel waits on memory once
+// for up to 64 splits; split indices past n_splits are clamped (the loads
+// stay inside the workspace) and their weights are zero.  The code is
+// branch-free straight-line work: the pass is latency-bound and each taken
+// branch or instruction-cache miss adds to it.
 template <int HD, int G>
 __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeParams p) {
-    constexpr int CH = kWave;
+    constexpr int CH = kWave;                       // splits per round
+    constexpr int RMAX = (kMaxSplits + CH - 1) / CH;  // (m, l) registers per lane
     const int g = blockIdx.x % G;
     const int kvh = (blockIdx.x / G) % p.n_head_kv;
     const int b = blockIdx.x / (G * p.n_head_kv);
@@ -765,46 +769,56 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     const int d = tid < HD ? tid : HD - 1;  // threads past HD (HD < 64) only load (m, l)
     const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
     const float *pg = p.part + head_base * p.n_splits * G * (HD + 4) + g * (HD + 4);
-    const int64_t sstride = (int64_t)G * (HD + 4);
+    const int sstride = G * (HD + 4);
     const int S = p.n_splits;
 
-    float o[CH], mv, lv;
+    float o[CH];
     auto load_round = [&](int s0) {
 #pragma unroll
-        for (int u = 0; u < CH; ++u) o[u] = s0 + u < S ? pg[(s0 + u) * sstride + d] : 0.0f;
-        const int sl = s0 + lane;
-        mv = sl < S ? pg[sl * sstride + HD] : -INFINITY;
-        lv = sl < S ? pg[sl * sstride + HD + 1] : 0.0f;
-    };
-    auto bcast = [](float x, int u) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), u));
+        for (int u = 0; u < CH; ++u) {
+            const float *row = pg + (int64_t)min(s0 + u, S - 1) * sstride;  // wave-uniform
+            o[u] = row[d];
+        }
     };
     load_round(0);
+    float mv[RMAX], lv[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+        const int s = min(CH * r + lane, S - 1);
+        mv[r] = pg[s * sstride + HD];
+        lv[r] = pg[s * sstride + HD + 1];
+    }
     int lo, n_kv, t0, n_tiles, tps, n_active;
     seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
     if (n_active <= 1) return;  // one split: written by the split pass
 
-    float M = -INFINITY, L = 0.0f, O = 0.0f;
-    for (int s0 = 0; s0 < n_active; s0 += CH) {
-        if (s0 > 0) load_round(s0);
-        float mc = M;
+    float mx = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < CH; ++u)
-            if (s0 + u < n_active) mc = fmaxf(mc, bcast(mv, u));
-        if (mc == -INFINITY) continue;
-        const float a = __builtin_amdgcn_exp2f(M - mc);  // M == -inf -> 0
-        L *= a;
-        O *= a;
+    for (int r = 0; r < RMAX; ++r) {
+        mv[r] = CH * r + lane < n_active ? mv[r] : -INFINITY;
+        mx = fmaxf(mx, mv[r]);
+    }
+    const float M = wave_max(mx);
+    float w[RMAX], lsum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+        w[r] = mv[r] != -INFINITY ? __builtin_amdgcn_exp2f(mv[r] - M) : 0.0f;
+        lsum += w[r] != 0.0f ? lv[r] * w[r] : 0.0f;
+    }
+    const float L = wave_sum(lsum);
+
+    // rows of splits >= n_active are not written by this call: their weight
+    // is zero and their (possibly stale) values are never multiplied
+    float O = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+        if (CH * r >= n_active) break;
+        if (r > 0) load_round(CH * r);
 #pragma unroll
         for (int u = 0; u < CH; ++u) {
-            if (s0 + u < n_active) {
-                const float m = bcast(mv, u);
-                const float wt = m != -INFINITY ? __builtin_amdgcn_exp2f(m - mc) : 0.0f;
-                L += bcast(lv, u) * wt;
-                O += o[u] * wt;
-            }
+            const float wt = lane_val(w[r], u);
+            O = wt != 0.0f ? fmaf(o[u], wt, O) : O;
         }
-        M = mc;
     }
     if (tid < HD) {
         float *out = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD;
@@ -828,7 +842,7 @@ SplitPlan plan_splits(int B, int Hkv, int max_seq_len) {
     const int wg_target = 512;
     int S = (wg_target + heads - 1) / heads;
     if (S < 1) S = 1;
-    if (S > 256) S = 256;
+    if (S > kMaxSplits) S = kMaxSplits;
     int tps = (tiles + S - 1) / S;
     if (tps < kDecodeWaves) tps = kDecodeWaves;
     S = (tiles + tps - 1) / tps;
