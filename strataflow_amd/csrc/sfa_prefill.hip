@@ -47,16 +47,18 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     constexpr int KC = HD / 16;
     constexpr int DB = HD / 32;
     constexpr int QB = 128 / G;           // query tokens per workgroup
-    constexpr int ROW = HD * 2 + 16;      // padded LDS row (bytes)
+    constexpr int ROW = HD * 2 + 64;      // padded LDS row (bytes)
     constexpr int CPR = HD / 8;           // 16-byte chunks per row
     constexpr int CHUNKS = kPBN * CPR;    // 16-byte chunks per tile
     constexpr int LPT = CHUNKS / 256;     // chunks per thread per tile
     static_assert(CHUNKS % 256 == 0, "tile chunks");
 
     // double-buffered K and V tiles.  K rows are unpadded with the 16-byte
-    // chunk c of row r stored at chunk c ^ (r % CPR), so the 32 rows an MFMA
-    // operand read touches spread over all banks; V rows are padded (the
-    // transposed reads walk rows).
+    // chunk c of row r stored at chunk c ^ (r % CPR), so the 16 rows one
+    // 16-lane slice of an MFMA operand read touches cover all 64 LDS banks.
+    // V rows are padded by 64 bytes: a transposed read's 32-lane half reads
+    // 64 bytes from each of four consecutive rows, which then start 16 banks
+    // apart (no bank conflicts).
     constexpr int KROW = HD * 2;
     __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * KROW];
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kPBN * ROW];
@@ -132,21 +134,28 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
 
     load(tile0);
 
+    // Q^T operand of this lane's row, rounded to f16; every chunk is loaded
+    // before any is converted (rows past T read row 0 and are zeroed), so
+    // the prologue waits on memory once
     half8 qf[KC];
     {
         const float *qr = p.q + ((int64_t)(row_ok ? tq : 0) * p.n_head + h) * HD;
+        floatx4 qx[KC][2];
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 16 * c + 8 * hh);
+            qx[c][0] = src[0];
+            qx[c][1] = src[1];
+        }
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
             half8 hv;
-            if (row_ok) {
-                const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 16 * c + 8 * hh);
-                const floatx4 x0 = src[0], x1 = src[1];
-                hv[0] = (_Float16)x0[0]; hv[1] = (_Float16)x0[1]; hv[2] = (_Float16)x0[2]; hv[3] = (_Float16)x0[3];
-                hv[4] = (_Float16)x1[0]; hv[5] = (_Float16)x1[1]; hv[6] = (_Float16)x1[2]; hv[7] = (_Float16)x1[3];
-            } else {
-                hv = half8{};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hv[e] = (_Float16)qx[c][0][e];
+                hv[4 + e] = (_Float16)qx[c][1][e];
             }
-            qf[c] = hv;
+            qf[c] = row_ok ? hv : half8{};
         }
     }
 
