@@ -600,15 +600,24 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
 #pragma unroll
                 for (int j = 0; j < 8; ++j) q[j] = r.vw[u][j + 1];
             }
-            const float dv = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
+            // q * d rounded to f16 on packed halves: byte b of a dword becomes
+            // the f16 1024 + (b ^ 0x80) (exponent byte 0x64 above it), minus
+            // 1152 gives q exactly, and one f16 multiply rounds q * d once,
+            // the same value as rounding the (exact) f32 product.  Rows
+            // outside [lo, n_kv) use d = 0 (their bytes may be anything).
+            const _Float16 dv = (interior || row_ok) ? __builtin_bit_cast(_Float16, (uint16_t)dbits) : (_Float16)0.0f;
+            const half2v dv2 = {dv, dv};
+            const half2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
             half8 h[4];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int qi = (int)(int8_t)((q[j] >> (8 * e)) & 0xffu);
-                    h[j >> 1][4 * (j & 1) + e] = (interior || row_ok) ? (_Float16)((float)qi * dv) : (_Float16)0.0f;
-                }
+                const uint32_t x = q[j] ^ 0x80808080u;
+                const half2v lo = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) + bias) * dv2;
+                const half2v hi = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) + bias) * dv2;
+                h[j >> 1][4 * (j & 1) + 0] = lo[0];
+                h[j >> 1][4 * (j & 1) + 1] = lo[1];
+                h[j >> 1][4 * (j & 1) + 2] = hi[0];
+                h[j >> 1][4 * (j & 1) + 3] = hi[1];
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k)
