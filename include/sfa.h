@@ -108,6 +108,22 @@ SFA_API int sfa_kv_append(const sfa_kv_desc *kv, const float *k, const float *v,
                           const int32_t *page_table, int32_t max_pages,
                           void *stream);
 
+/* Fused RoPE + KV append: the rope_ext of Qcur and Kcur (engine.cpp:1892-1897:
+ * ggml_rope_ext mode NORMAL, n_dims = head_dim, freq_base, freq_scale 1,
+ * ext_factor 0, attn_factor 1) followed by the append of sfa_kv_append
+ * (engine.cpp:1646-1656), in one pass.  q: [n_tok][n_head][head_dim] f32 pre-RoPE,
+ * rotated in place (may be NULL: K and V only); k: [n_tok][n_head_kv][head_dim]
+ * f32 pre-RoPE (not modified; its rotation goes only into the cache, as Kcur's
+ * does in the reference); v: raw V.  Pair (x[2i], x[2i+1]) rotates by theta_i,
+ * theta_0 = pos and theta_{i+1} = theta_i * powf(freq_base, -2/head_dim) in f32
+ * (ggml's recurrence), with cosf/sinf.  The rotated K is converted exactly as
+ * sfa_kv_append converts.  A token with seq < 0 or pos < 0 is skipped (its Q
+ * row untouched).  head_dim <= 128. */
+SFA_API int sfa_rope_kv_append(const sfa_kv_desc *kv, float *q, const float *k, const float *v,
+                               const int32_t *seq, const int32_t *pos, int32_t n_tok,
+                               const int32_t *page_table, int32_t max_pages, float freq_base,
+                               void *stream);
+
 /* Workspace bytes needed by sfa_attn_decode for B sequences with the given
  * max_seq_len (the bound on the attended span, see sfa_attn_decode). */
 SFA_API size_t sfa_decode_workspace_bytes(const sfa_kv_desc *kv, int32_t B,

@@ -80,6 +80,13 @@ SFA_API int sfa_pager_begin(sfa_pager *pager, const int32_t *n_tok, void *stream
 SFA_API int sfa_pager_append(sfa_pager *pager, int32_t layer, const float *k, const float *v,
                              void *stream);
 
+/* sfa_pager_append with the RoPE of Qcur and Kcur fused in (sfa_rope_kv_append,
+ * engine.cpp:1892-1897 then :1646-1656): q [n_tokens][n_head][head_dim] f32
+ * device pre-RoPE, rotated in place for sfa_pager_attend (may be NULL); k
+ * pre-RoPE, v raw. */
+SFA_API int sfa_pager_rope_append(sfa_pager *pager, int32_t layer, float *q, const float *k,
+                                  const float *v, float freq_base, void *stream);
+
 /* Attention of the step's tokens over one layer: q [n_tokens][n_head][head_dim]
  * f32 device, out [n_tokens][n_head * head_dim] f32 device.  A step with one
  * token per sequence runs sfa_attn_decode over the batch (split plan sized for

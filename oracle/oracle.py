@@ -170,5 +170,15 @@ class HostPagedKv:
         return float(np.median(ts))
 
 
+def rope_normal(x: np.ndarray, pos: np.ndarray, freq_base: float) -> np.ndarray:
+    """RoPE NORMAL of x [n_tok, n_heads, head_dim] (a rotated copy), through
+    orc_rope_normal (ggml's f32 theta recurrence, engine.cpp:1892-1897)."""
+    y = _c(x, np.float32).copy()
+    pos = _c(pos, np.int32)
+    n_tok, n_heads, hd = y.shape
+    load().orc_rope_normal(y.ctypes.data, pos.ctypes.data, n_tok, n_heads, hd, float(freq_base))
+    return y
+
+
 def max_threads() -> int:
     return int(load().orc_max_threads())

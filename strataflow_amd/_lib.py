@@ -29,6 +29,7 @@ EXPORTS = (
     "sfa_page_bytes",
     "sfa_kv_desc_check",
     "sfa_kv_append",
+    "sfa_rope_kv_append",
     "sfa_decode_workspace_bytes",
     "sfa_workspace_init",
     "sfa_attn_decode",
@@ -92,6 +93,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_kv_desc_check.restype = ctypes.c_int
     lib.sfa_kv_append.argtypes = [D, P, P, P, P, i32, P, i32, P]
     lib.sfa_kv_append.restype = ctypes.c_int
+    lib.sfa_rope_kv_append.argtypes = [D, P, P, P, P, P, i32, P, i32, ctypes.c_float, P]
+    lib.sfa_rope_kv_append.restype = ctypes.c_int
     lib.sfa_decode_workspace_bytes.argtypes = [D, i32, i32]
     lib.sfa_decode_workspace_bytes.restype = ctypes.c_size_t
     lib.sfa_workspace_init.argtypes = [P, ctypes.c_size_t, P]
@@ -133,6 +136,7 @@ HOST_EXPORTS = (
     "sfa_pager_destroy",
     "sfa_pager_begin",
     "sfa_pager_append",
+    "sfa_pager_rope_append",
     "sfa_pager_attend",
     "sfa_pager_reset",
     "sfa_pager_stats_get",
@@ -194,6 +198,8 @@ def load_host(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_pager_begin.restype = ctypes.c_int
     lib.sfa_pager_append.argtypes = [P, i32, P, P, P]
     lib.sfa_pager_append.restype = ctypes.c_int
+    lib.sfa_pager_rope_append.argtypes = [P, i32, P, P, P, ctypes.c_float, P]
+    lib.sfa_pager_rope_append.restype = ctypes.c_int
     lib.sfa_pager_attend.argtypes = [P, i32, P, P, P]
     lib.sfa_pager_attend.restype = ctypes.c_int
     lib.sfa_pager_reset.argtypes = [P, i32, P]

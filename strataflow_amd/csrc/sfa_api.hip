@@ -18,6 +18,10 @@ int prefill_launch(const sfa_kv_desc *kv, const float *q, float *out, const int3
 int append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const int32_t *seq,
                   const int32_t *pos, int32_t n_tok, const int32_t *page_table, int32_t max_pages,
                   hipStream_t stream);
+int rope_append_launch(const sfa_kv_desc *kv, float *q, const float *k, const float *v,
+                       const int32_t *seq, const int32_t *pos, int32_t n_tok,
+                       const int32_t *page_table, int32_t max_pages, float freq_base,
+                       hipStream_t stream);
 int workspace_init_launch(void *ws, size_t bytes, hipStream_t stream);
 }  // namespace sfa
 
@@ -77,6 +81,22 @@ SFA_API int sfa_kv_append(const sfa_kv_desc *kv, const float *k, const float *v,
         if (rc != SFA_OK) return rc;
         return sfa::append_launch(kv, k, v, seq, pos, n_tok, page_table, max_pages,
                                   static_cast<hipStream_t>(stream));
+    } catch (const std::exception &) {
+        return SFA_ERR_RUNTIME;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
+SFA_API int sfa_rope_kv_append(const sfa_kv_desc *kv, float *q, const float *k, const float *v,
+                               const int32_t *seq, const int32_t *pos, int32_t n_tok,
+                               const int32_t *page_table, int32_t max_pages, float freq_base,
+                               void *stream) {
+    try {
+        const int rc = check_desc(kv);
+        if (rc != SFA_OK) return rc;
+        return sfa::rope_append_launch(kv, q, k, v, seq, pos, n_tok, page_table, max_pages, freq_base,
+                                       static_cast<hipStream_t>(stream));
     } catch (const std::exception &) {
         return SFA_ERR_RUNTIME;
     } catch (...) {

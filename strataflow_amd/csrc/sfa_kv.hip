@@ -49,6 +49,45 @@ __device__ inline uint8_t *row_ptr(const AppendParams &p, int which, int tok, in
     return base + ((int64_t)(ps - lp * p.page_size) * p.n_head_kv + kvh) * p.row_bytes;
 }
 
+// 8 consecutive elements of a row -> f16 (RNE), one 16-byte store.
+__device__ inline void store_f16x8(uint8_t *dst, const float (&x)[8]) {
+    half8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (_Float16)x[j];
+    *reinterpret_cast<half8 *>(dst) = h;
+}
+
+// One 32-element block -> block_q8_0 (quantize_row_q8_0 semantics): d =
+// amax / 127 stored fp16, q = round(x * (1/d)).  The block starts 2-byte
+// aligned: d and the quants are stored as 16-bit words.
+__device__ inline void store_q8_block(uint8_t *blkp, const float (&x)[kQK]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kQK; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const _Float16 dh = (_Float16)d;
+    uint16_t dbits;
+    __builtin_memcpy(&dbits, &dh, 2);
+    uint16_t *w = reinterpret_cast<uint16_t *>(blkp);
+    w[0] = dbits;
+#pragma unroll
+    for (int j = 0; j < kQK; j += 2) {
+        const int q0 = (int)roundf(x[j] * id);
+        const int q1 = (int)roundf(x[j + 1] * id);
+        w[1 + j / 2] = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+    }
+}
+
+template <int N>
+__device__ inline void load_f32(const float *src, float (&x)[N]) {
+#pragma unroll
+    for (int j = 0; j < N; j += 4) {
+        const floatx4 v4 = reinterpret_cast<const floatx4 *>(src + j)[0];
+        x[j] = v4[0]; x[j + 1] = v4[1]; x[j + 2] = v4[2]; x[j + 3] = v4[3];
+    }
+}
+
 // One thread per 8 elements of a row: f32 -> f16 (RNE), 16-byte store.
 __global__ __launch_bounds__(256) void append_f16_kernel(AppendParams p) {
     const int chunks = p.head_dim / 8;
@@ -63,13 +102,9 @@ __global__ __launch_bounds__(256) void append_f16_kernel(AppendParams p) {
     const int tok = (int)(r / p.n_head_kv);
     uint8_t *dst = row_ptr(p, which, tok, kvh);
     if (dst == nullptr) return;
-    const float *src = (which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + 8 * c;
-    const floatx4 a = reinterpret_cast<const floatx4 *>(src)[0];
-    const floatx4 bq = reinterpret_cast<const floatx4 *>(src)[1];
-    half8 h;
-    h[0] = (_Float16)a[0]; h[1] = (_Float16)a[1]; h[2] = (_Float16)a[2]; h[3] = (_Float16)a[3];
-    h[4] = (_Float16)bq[0]; h[5] = (_Float16)bq[1]; h[6] = (_Float16)bq[2]; h[7] = (_Float16)bq[3];
-    *reinterpret_cast<half8 *>(dst + 16 * c) = h;
+    float x[8];
+    load_f32<8>((which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + 8 * c, x);
+    store_f16x8(dst + 16 * c, x);
 }
 
 // One thread per 32-element block: quantize_row_q8_0 semantics.
@@ -86,30 +121,74 @@ __global__ __launch_bounds__(256) void append_q8_0_kernel(AppendParams p) {
     const int tok = (int)(r / p.n_head_kv);
     uint8_t *dst = row_ptr(p, which, tok, kvh);
     if (dst == nullptr) return;
-    const float *src = (which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + kQK * blk;
     float x[kQK];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kQK; j += 4) {
-        const floatx4 v4 = reinterpret_cast<const floatx4 *>(src + j)[0];
-        x[j] = v4[0]; x[j + 1] = v4[1]; x[j + 2] = v4[2]; x[j + 3] = v4[3];
+    load_f32<kQK>((which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + kQK * blk, x);
+    store_q8_block(dst + kQ8Bytes * blk, x);
+}
+
+// Fused RoPE NORMAL + KV append (engine.cpp:1892-1897, then :1646-1656), one
+// workgroup per token.  ggml_rope_ext mode 0 with n_dims = head_dim,
+// freq_scale 1, ext_factor 0, attn_factor 1: pair (x[2i], x[2i+1]) rotates by
+// theta_i, where theta_0 = pos and theta_{i+1} = theta_i * theta_scale in f32
+// (ggml's recurrence, theta_scale = powf(freq_base, -2/n_dims) computed on the
+// host), with cosf / sinf of theta_i.  Q rotates in place; K rotates on its
+// way into the cache (converted as the append converts); V is appended raw.
+// A token with seq < 0 or pos < 0 is skipped entirely (Q untouched).
+constexpr int kMaxHalfDim = 64;
+template <int KVT>
+__global__ __launch_bounds__(256) void rope_append_kernel(AppendParams p, float *q, int n_head,
+                                                          float theta_scale) {
+    __shared__ float cs[kMaxHalfDim][2];
+    const int tok = blockIdx.x;
+    const int ps = p.pos[tok];
+    if (ps < 0 || p.seq[tok] < 0) return;  // workgroup-uniform: before any barrier
+    const int half = p.head_dim / 2;
+    if ((int)threadIdx.x < half) {
+        float theta = (float)ps;
+        for (int j = 0; j < (int)threadIdx.x; ++j) theta *= theta_scale;
+        cs[threadIdx.x][0] = cosf(theta);
+        cs[threadIdx.x][1] = sinf(theta);
     }
+    __syncthreads();
+    auto rot = [&](float (&x)[2], int i) {
+        const float c = cs[i][0], s = cs[i][1];
+        const float x0 = x[0], x1 = x[1];
+        x[0] = x0 * c - x1 * s;
+        x[1] = x0 * s + x1 * c;
+    };
+    if (q != nullptr) {
+        for (int idx = threadIdx.x; idx < n_head * half; idx += blockDim.x) {
+            const int h = idx / half, i = idx % half;
+            float *r = q + ((int64_t)tok * n_head + h) * p.head_dim + 2 * i;
+            float x[2] = {r[0], r[1]};
+            rot(x, i);
+            r[0] = x[0];
+            r[1] = x[1];
+        }
+    }
+    constexpr int E = KVT == SFA_KV_F16 ? 8 : kQK;  // elements per unit of work
+    const int units = p.head_dim / E;
+    for (int idx = threadIdx.x; idx < 2 * p.n_head_kv * units; idx += blockDim.x) {
+        const int which = idx / (p.n_head_kv * units);
+        const int r = idx % (p.n_head_kv * units);
+        const int kvh = r / units, u = r % units;
+        uint8_t *dst = row_ptr(p, which, tok, kvh);
+        if (dst == nullptr) continue;
+        float x[E];
+        load_f32<E>((which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + E * u, x);
+        if (which == 0) {
 #pragma unroll
-    for (int j = 0; j < kQK; ++j) amax = fmaxf(amax, fabsf(x[j]));
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint8_t *blkp = dst + kQ8Bytes * blk;
-    const _Float16 dh = (_Float16)d;
-    uint16_t dbits;
-    __builtin_memcpy(&dbits, &dh, 2);
-    // the block starts 2-byte aligned: store d and the quants as 16-bit words
-    uint16_t *w = reinterpret_cast<uint16_t *>(blkp);
-    w[0] = dbits;
-#pragma unroll
-    for (int j = 0; j < kQK; j += 2) {
-        const int q0 = (int)roundf(x[j] * id);
-        const int q1 = (int)roundf(x[j + 1] * id);
-        w[1 + j / 2] = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+            for (int j = 0; j < E; j += 2) {
+                float pr[2] = {x[j], x[j + 1]};
+                rot(pr, (E * u + j) / 2);
+                x[j] = pr[0];
+                x[j + 1] = pr[1];
+            }
+        }
+        if constexpr (KVT == SFA_KV_F16)
+            store_f16x8(dst + 16 * u, x);
+        else
+            store_q8_block(dst + kQ8Bytes * u, x);
     }
 }
 
@@ -118,13 +197,9 @@ __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
     if (i < n_words) p[i] = 0u;
 }
 
-int append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const int32_t *seq,
-                  const int32_t *pos, int32_t n_tok, const int32_t *page_table, int32_t max_pages,
-                  hipStream_t stream) {
-    if (n_tok < 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
-    if (n_tok == 0) return SFA_OK;
-    if (k == nullptr || v == nullptr || seq == nullptr || pos == nullptr || page_table == nullptr)
-        return SFA_ERR_INVALID_ARGUMENT;
+static AppendParams append_params(const sfa_kv_desc *kv, const float *k, const float *v,
+                                  const int32_t *seq, const int32_t *pos, int32_t n_tok,
+                                  const int32_t *page_table, int32_t max_pages) {
     AppendParams p;
     p.k_pages = static_cast<uint8_t *>(kv->k_pages);
     p.v_pages = static_cast<uint8_t *>(kv->v_pages);
@@ -144,6 +219,17 @@ int append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const i
     p.n_tok = n_tok;
     p.page_table = page_table;
     p.max_pages = max_pages;
+    return p;
+}
+
+int append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const int32_t *seq,
+                  const int32_t *pos, int32_t n_tok, const int32_t *page_table, int32_t max_pages,
+                  hipStream_t stream) {
+    if (n_tok < 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
+    if (n_tok == 0) return SFA_OK;
+    if (k == nullptr || v == nullptr || seq == nullptr || pos == nullptr || page_table == nullptr)
+        return SFA_ERR_INVALID_ARGUMENT;
+    AppendParams p = append_params(kv, k, v, seq, pos, n_tok, page_table, max_pages);
     int64_t total;
     if (kv->kv_type == SFA_KV_F16) {
         total = (int64_t)n_tok * kv->n_head_kv * (kv->head_dim / 8) * 2;
@@ -165,6 +251,30 @@ int workspace_init_launch(void *ws, size_t bytes, hipStream_t stream) {
     if (words == 0) return SFA_OK;
     hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
                        static_cast<uint32_t *>(ws), words);
+    return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+}
+
+int rope_append_launch(const sfa_kv_desc *kv, float *q, const float *k, const float *v,
+                       const int32_t *seq, const int32_t *pos, int32_t n_tok,
+                       const int32_t *page_table, int32_t max_pages, float freq_base,
+                       hipStream_t stream) {
+    if (n_tok < 0 || max_pages <= 0 || !(freq_base > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
+    if (n_tok == 0) return SFA_OK;
+    if (k == nullptr || v == nullptr || seq == nullptr || pos == nullptr || page_table == nullptr)
+        return SFA_ERR_INVALID_ARGUMENT;
+    if (kv->head_dim / 2 > kMaxHalfDim) return SFA_ERR_UNSUPPORTED;
+    AppendParams p = append_params(kv, k, v, seq, pos, n_tok, page_table, max_pages);
+    // ggml: theta_scale = powf(freq_base, -2.0f/n_dims)
+    const float theta_scale = powf(freq_base, -2.0f / (float)kv->head_dim);
+    if (kv->kv_type == SFA_KV_F16) {
+        hipLaunchKernelGGL(rope_append_kernel<SFA_KV_F16>, dim3((unsigned)n_tok), dim3(256), 0, stream, p, q,
+                           kv->n_head, theta_scale);
+    } else if (kv->kv_type == SFA_KV_Q8_0) {
+        hipLaunchKernelGGL(rope_append_kernel<SFA_KV_Q8_0>, dim3((unsigned)n_tok), dim3(256), 0, stream, p, q,
+                           kv->n_head, theta_scale);
+    } else {
+        return SFA_ERR_UNSUPPORTED;
+    }
     return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
 }
 

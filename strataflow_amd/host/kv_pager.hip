@@ -283,6 +283,15 @@ SFA_API int sfa_pager_append(sfa_pager *p, int32_t layer, const float *k, const 
                          p->d_table, p->max_pages, stream);
 }
 
+SFA_API int sfa_pager_rope_append(sfa_pager *p, int32_t layer, float *q, const float *k,
+                                  const float *v, float freq_base, void *stream) {
+    if (p == nullptr || !p->step_open || layer < 0 || layer >= p->cfg.n_layer)
+        return SFA_ERR_INVALID_ARGUMENT;
+    if (p->step_tokens == 0) return SFA_OK;
+    return sfa_rope_kv_append(&p->descs[layer], q, k, v, p->d_tok_seq, p->d_tok_pos, p->step_tokens,
+                              p->d_table, p->max_pages, freq_base, stream);
+}
+
 SFA_API int sfa_pager_attend(sfa_pager *p, int32_t layer, const float *q, float *out,
                              void *stream) {
     if (p == nullptr || !p->step_open || layer < 0 || layer >= p->cfg.n_layer)

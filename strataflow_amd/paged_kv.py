@@ -112,6 +112,24 @@ class PagedKV:
                                      pos.data_ptr(), n_tok, page_table.data_ptr(),
                                      int(page_table.shape[-1]), _stream(stream)), "sfa_kv_append")
 
+    def rope_append(self, layer: int, q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
+                    seq: torch.Tensor, pos: torch.Tensor, page_table: torch.Tensor, freq_base: float,
+                    stream=None) -> None:
+        """Fused RoPE NORMAL + append: q [n_tok, Hq, hd] (rotated in place, or
+        None), k pre-RoPE and v raw [n_tok, Hkv, hd] f32 on device."""
+        n_tok = int(seq.numel())
+        assert k.is_contiguous() and v.is_contiguous() and k.dtype == torch.float32
+        assert k.shape == (n_tok, self.n_head_kv, self.head_dim) and v.shape == k.shape
+        if q is not None:
+            assert q.is_contiguous() and q.dtype == torch.float32
+            assert q.shape == (n_tok, self.n_head, self.head_dim)
+        lib = _lib.load()
+        d = self.desc(layer)
+        _lib.check(lib.sfa_rope_kv_append(ctypes.byref(d), _ptr(q), k.data_ptr(), v.data_ptr(),
+                                          seq.data_ptr(), pos.data_ptr(), n_tok, page_table.data_ptr(),
+                                          int(page_table.shape[-1]), float(freq_base), _stream(stream)),
+                   "sfa_rope_kv_append")
+
     def decode(self, layer: int, q: torch.Tensor, page_table: torch.Tensor, seq_len: torch.Tensor,
                max_seq_len: int, kv_lo: torch.Tensor | None = None, out: torch.Tensor | None = None,
                scale: float | None = None, stream=None, split_end_event=None) -> torch.Tensor:

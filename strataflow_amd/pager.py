@@ -71,6 +71,17 @@ class KvPager:
         _lib.check(_lib.load_host().sfa_pager_append(self._h, layer, k.data_ptr(), v.data_ptr(),
                                                      _stream()), "sfa_pager_append")
 
+    def rope_append(self, layer: int, q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
+                    freq_base: float) -> None:
+        """Fused RoPE NORMAL + append: q (rotated in place, or None) and k pre-RoPE."""
+        assert k.is_contiguous() and v.is_contiguous() and k.dtype == torch.float32
+        assert k.shape == (self.n_tokens, self.n_head_kv, self.head_dim) and v.shape == k.shape
+        if q is not None:
+            assert q.is_contiguous() and q.shape == (self.n_tokens, self.n_head, self.head_dim)
+        _lib.check(_lib.load_host().sfa_pager_rope_append(
+            self._h, layer, None if q is None else q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            float(freq_base), _stream()), "sfa_pager_rope_append")
+
     def attend(self, layer: int, q: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         assert q.is_contiguous() and q.dtype == torch.float32
         assert q.shape == (self.n_tokens, self.n_head, self.head_dim)

@@ -7,7 +7,25 @@ order never equals physical order.
 """
 from __future__ import annotations
 
+import ctypes
+import ctypes.util
+
 import numpy as np
+
+
+def powf(x: float, y: float) -> np.float32:
+    """C's powf, the f32 pow ggml uses for theta_scale; the theta recurrence
+    amplifies a one-ulp difference in its factor, so numpy's float32 power is
+    not used for it."""
+    global _libm
+    if _libm is None:
+        _libm = ctypes.CDLL(ctypes.util.find_library("m"))
+        _libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+        _libm.powf.restype = ctypes.c_float
+    return np.float32(_libm.powf(float(x), float(y)))
+
+
+_libm = None
 
 
 def rope_normal(x: np.ndarray, pos: np.ndarray, freq_base: float) -> np.ndarray:
@@ -18,7 +36,7 @@ def rope_normal(x: np.ndarray, pos: np.ndarray, freq_base: float) -> np.ndarray:
     theta follows ggml's float32 recurrence theta *= base^(-2/hd)."""
     x = np.asarray(x, dtype=np.float32)
     n_tok, _, hd = x.shape
-    theta_scale = np.float32(np.power(np.float32(freq_base), np.float32(-2.0) / np.float32(hd)))
+    theta_scale = powf(np.float32(freq_base), np.float32(-2.0) / np.float32(hd))
     theta = np.empty((n_tok, hd // 2), dtype=np.float32)
     cur = np.asarray(pos, dtype=np.float32).copy()
     for i in range(hd // 2):
@@ -78,7 +96,7 @@ def rope_normal_torch(x, pos, freq_base: float):
     """rope_normal on a torch tensor x [n_tok, n_heads, head_dim] (device)."""
     import torch
     n_tok, _, hd = x.shape
-    theta_scale = float(np.float32(np.power(np.float32(freq_base), np.float32(-2.0) / np.float32(hd))))
+    theta_scale = float(powf(np.float32(freq_base), np.float32(-2.0) / np.float32(hd)))
     i = torch.arange(hd // 2, device=x.device, dtype=torch.float64)
     theta = (pos.to(torch.float64)[:, None] * torch.pow(torch.tensor(theta_scale, dtype=torch.float64,
                                                                       device=x.device), i)).float()

@@ -122,9 +122,11 @@ class TinyMoe:
             q = (cur @ L["wq"].T).reshape(T, cfg.n_head, cfg.head_dim)
             k = (cur @ L["wk"].T).reshape(T, cfg.n_head_kv, cfg.head_dim)
             v = (cur @ L["wv"].T).reshape(T, cfg.n_head_kv, cfg.head_dim)
-            q = synth.rope_normal(q, pos, cfg.freq_base)
-            k = synth.rope_normal(k, pos, cfg.freq_base)
-            attn = self.attention(il, q, k, np.ascontiguousarray(v), pos0)
+            if not getattr(self.attention, "applies_rope", False):
+                q = synth.rope_normal(q, pos, cfg.freq_base)
+                k = synth.rope_normal(k, pos, cfg.freq_base)
+            attn = self.attention(il, np.ascontiguousarray(q), np.ascontiguousarray(k),
+                                  np.ascontiguousarray(v), pos0)
             ffn_inp = (attn @ L["wo"].T + x).astype(np.float32)
             cur = rms_norm(ffn_inp, cfg.rms_eps) * L["ffn_norm"]
             x = (moe_ffn(L, cur, cfg) + ffn_inp).astype(np.float32)
@@ -153,9 +155,13 @@ class TinyMoe:
 class HipAttention:
     """The attention node on the GPU through libsfa.so: per layer a paged f16
     cache (one 256-token page per sequence here), sfa_kv_append, then
-    sfa_attn_decode (one token) or sfa_attn_prefill (a chunk)."""
+    sfa_attn_decode (one token) or sfa_attn_prefill (a chunk).  With
+    ``fused_rope`` it receives Q and K before RoPE and runs sfa_rope_kv_append
+    (RoPE of Q and K fused with the append) instead."""
 
-    def __init__(self, cfg: TinyMoeConfig, n_ctx: int, device: str = "cuda", seed: int = 0):
+    def __init__(self, cfg: TinyMoeConfig, n_ctx: int, device: str = "cuda", seed: int = 0,
+                 fused_rope: bool = False):
+        self.applies_rope = fused_rope
         import torch
 
         from .paged_kv import SFA_KV_F16, PagedKV
@@ -175,9 +181,13 @@ class HipAttention:
         dev = self.device
         pos = torch.arange(pos0, pos0 + T, dtype=torch.int32, device=dev)
         seq = torch.zeros(T, dtype=torch.int32, device=dev)
-        self.kv.append(layer, torch.from_numpy(np.ascontiguousarray(k)).to(dev),
-                       torch.from_numpy(np.ascontiguousarray(v)).to(dev), seq, pos, self.pt)
+        tk = torch.from_numpy(np.ascontiguousarray(k)).to(dev)
+        tv = torch.from_numpy(np.ascontiguousarray(v)).to(dev)
         tq = torch.from_numpy(np.ascontiguousarray(q)).to(dev)
+        if self.applies_rope:
+            self.kv.rope_append(layer, tq, tk, tv, seq, pos, self.pt, self.cfg.freq_base)
+        else:
+            self.kv.append(layer, tk, tv, seq, pos, self.pt)
         if T == 1:
             sl = torch.tensor([pos0 + 1], dtype=torch.int32, device=dev)
             out = self.kv.decode(layer, tq, self.pt, sl, self.n_ctx)

@@ -195,3 +195,42 @@ def test_pager_window_4096_history_65536(gpu, attend):
         assert st["cold_pages_in_use"] == st["pages_evicted"] > 4 * 230
     else:
         assert st["pages_dropped"] > 4 * 230 and st["cold_pages_in_use"] == 0
+
+
+def test_pager_rope_append_matches_full(gpu):
+    """sfa_pager_rope_append (pre-RoPE Q and K) against the full-resident cache
+    fed through sfa_rope_kv_append: the rotated Q rows and the attention
+    outputs are bit-identical while pages leave the window."""
+    n_seq, n_ctx, window, P, Hq, Hkv, hd = 2, 2048, 512, 256, 32, 8, 128
+    pager = KvPager(n_layer=1, n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=SFA_KV_F16,
+                    page_size=P, n_seq=n_seq, n_ctx=n_ctx, window=window,
+                    attend=SFA_ATTEND_LOSSLESS, seed=5)
+    rng = np.random.default_rng(5)
+    max_pages = n_ctx // P
+    n_pages = n_seq * max_pages + 2
+    full = PagedKV(1, Hq, Hkv, hd, SFA_KV_F16, P, n_pages)
+    pt = torch.from_numpy(synth.page_tables(rng, [n_ctx] * n_seq, P, n_pages, max_pages)).cuda()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    used = np.zeros(n_seq, np.int64)
+    for step in range(12):
+        n_tok = np.array([P, P // 2], np.int32) if step < 5 else np.ones(n_seq, np.int32)
+        assert pager.begin(n_tok) == 0
+        seq = np.concatenate([np.full(n, b, np.int32) for b, n in enumerate(n_tok)])
+        pos = np.concatenate([used[b] + np.arange(n) for b, n in enumerate(n_tok)]).astype(np.int32)
+        n = int(n_tok.sum())
+        k = torch.randn((n, Hkv, hd), generator=gen, device="cuda")
+        v = torch.randn((n, Hkv, hd), generator=gen, device="cuda")
+        q = torch.randn((n, Hq, hd), generator=gen, device="cuda")
+        q_pager, q_full = q.clone(), q.clone()
+        pager.rope_append(0, q_pager, k, v, 1e6)
+        full.rope_append(0, q_full, k, v, torch.from_numpy(seq).cuda(), torch.from_numpy(pos).cuda(), pt, 1e6)
+        used += n_tok
+        assert torch.equal(q_pager, q_full)
+        if step >= 5:
+            out = pager.attend(0, q_pager)
+            ref = full.decode(0, q_full.view(n_seq, Hq, hd), pt, torch.from_numpy(used.astype(np.int32)).cuda(),
+                              n_ctx)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"step {step}: paged != full-resident"
+    assert pager.stats()["pages_evicted"] > 0

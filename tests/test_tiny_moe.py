@@ -40,17 +40,18 @@ def test_tiny_moe_oracle_modes_agree(oracle_mod):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fused_rope", [False, True], ids=["host_rope", "fused_rope_append"])
 @pytest.mark.parametrize("chunked", [False, True], ids=["per_token_prompt", "chunked_prompt"])
-def test_tiny_moe_greedy_identical(gpu, oracle_mod, chunked):
+def test_tiny_moe_greedy_identical(gpu, oracle_mod, chunked, fused_rope):
     cfg = TinyMoeConfig()
     w = TinyMoeWeights(cfg, seed=0)
     n_ctx = N_PROMPT + N_GEN
     ref = TinyMoe(cfg, w, OracleAttention(oracle_mod, cfg, n_ctx, oracle_mod.GGML)).generate(
         _prompt(cfg), N_GEN, chunked_prompt=chunked)
-    got = TinyMoe(cfg, w, HipAttention(cfg, n_ctx, device=gpu)).generate(
+    got = TinyMoe(cfg, w, HipAttention(cfg, n_ctx, device=gpu, fused_rope=fused_rope)).generate(
         _prompt(cfg), N_GEN, chunked_prompt=chunked)
     same, dl, margin = _compare(ref, got)
-    print(f"\n[tiny-moe chunked={chunked}] seq match={same} max per-step |dlogit|={dl:.3e} "
+    print(f"\n[tiny-moe chunked={chunked} fused_rope={fused_rope}] seq match={same} max per-step |dlogit|={dl:.3e} "
           f"min top-2 margin={margin:.3e} tokens={got[0]}")
     assert same, (ref[0], got[0])
     assert dl < 1e-3
