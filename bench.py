@@ -400,6 +400,92 @@ def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 4):
     return res
 
 
+def rope_bench(torch, steps: int, seed: int):
+    """Fused RoPE + KV append (sfa_rope_kv_append): a decode step (B=1, one
+    token per layer, 32 layers in a HIP graph) and a 2048-token prefill chunk
+    at positions 2048..4095 (8 layers with distinct caches), f16 cache,
+    RoPE base 1e6."""
+    from strataflow_amd import synth
+    from strataflow_amd.paged_kv import PagedKV, SFA_KV_F16
+    dev = torch.device("cuda:0")
+    res = {}
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+
+    # decode step: one token at position 4095 per layer
+    n_kv = 4096
+    pool = n_kv // PAGE + 1
+    kv = PagedKV(N_LAYER, HQ, HKV, HD, SFA_KV_F16, PAGE, pool, device=dev)
+    pt = torch.from_numpy(synth.page_tables(rng, [n_kv], PAGE, pool)).to(dev)
+    seq = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.full((1,), n_kv - 1, dtype=torch.int32, device=dev)
+    qs = torch.randn((N_LAYER, 1, HQ, HD), device=dev, generator=gen)
+    ks = torch.randn((N_LAYER, 1, HKV, HD), device=dev, generator=gen)
+    vs = torch.randn((N_LAYER, 1, HKV, HD), device=dev, generator=gen)
+
+    def step():
+        for layer in range(N_LAYER):
+            kv.rope_append(layer, qs[layer], ks[layer], vs[layer], seq, pos, pt, 1e6)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps / N_LAYER
+    res["decode_b1"] = {
+        "workload": "fused RoPE (base 1e6) of Q [1,32,128] and K [1,8,128] + append of K, V into an "
+                    "f16 paged cache at position 4095, 32 layers in a HIP graph",
+        "us_per_layer_token": round(us, 3),
+    }
+    del kv, qs, ks, vs, g
+    torch.cuda.empty_cache()
+
+    # prefill chunk: 2048 tokens at positions 2048..4095
+    T, n_layer = 2048, 8
+    kv = PagedKV(n_layer, HQ, HKV, HD, SFA_KV_F16, PAGE, pool, device=dev)
+    pos = torch.arange(n_kv - T, n_kv, dtype=torch.int32, device=dev)
+    seq = torch.zeros(T, dtype=torch.int32, device=dev)
+    qs = torch.randn((n_layer, T, HQ, HD), device=dev, generator=gen)
+    ks = torch.randn((n_layer, T, HKV, HD), device=dev, generator=gen)
+    vs = torch.randn((n_layer, T, HKV, HD), device=dev, generator=gen)
+    for layer in range(n_layer):
+        kv.rope_append(layer, qs[layer], ks[layer], vs[layer], seq, pos, pt, 1e6)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        for layer in range(n_layer):
+            kv.rope_append(layer, qs[layer], ks[layer], vs[layer], seq, pos, pt, 1e6)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps / n_layer
+    # Q read + written, K and V read, K and V f16 rows written, each once
+    alg = 2 * T * HQ * HD * 4 + 2 * T * HKV * HD * 4 + 2 * T * HKV * HD * 2
+    gbs = alg / (us * 1e-6) / 1e9
+    res["prefill_2048"] = {
+        "workload": "fused RoPE (base 1e6) of Q [2048,32,128] and K [2048,8,128] + append of K, V "
+                    "into an f16 paged cache at positions 2048..4095, 8 layers with distinct caches",
+        "us_per_layer_chunk": round(us, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "rope_append_kernel<f16>", "bytes_per_launch": alg},
+    }
+    del kv, qs, ks, vs
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(kv, pt, q_layer0, ctx, budget_s=12.0):
     """The oracle (ggml semantics, the reference's op sequence with its three
     history copies) on the host cores, layer 0 of the same workload."""
@@ -436,7 +522,8 @@ def main():
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 decode legs")
     ap.add_argument("--no-window", action="store_true", help="skip the KV-window paging legs")
     ap.add_argument("--no-32k", action="store_true", help="skip the f16 context-32768 decode leg")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window"],
+    ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE + append leg")
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope"],
                     help="run one leg only and print its JSON (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
@@ -465,7 +552,7 @@ def main():
         return
 
     if args.only == "decode4k":
-        args.no_prefill = args.no_q8 = args.no_window = args.no_32k = args.no_cpu = True
+        args.no_prefill = args.no_q8 = args.no_window = args.no_32k = args.no_cpu = args.no_rope = True
     if args.only and args.only != "decode4k":
         if args.only == "decode32k":
             r = decode_leg(torch, "decode_f16_ctx32k", [32768], 1, max(args.steps // 4, 5), 3, args.seed + 4)
@@ -473,6 +560,8 @@ def main():
             r = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2)
         elif args.only == "prefill":
             r = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1)
+        elif args.only == "rope":
+            r = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
         else:
             r = window_bench(torch, args.seed + 3)
         print(json.dumps({args.only: r}))
@@ -525,6 +614,8 @@ def main():
         result["q8_0"] = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2)
     if not args.no_window:
         result["window"] = window_bench(torch, args.seed + 3)
+    if not args.no_rope:
+        result["rope_append"] = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
     result["hbm_copy_ceiling"] = copy_ceiling(torch)
     if not args.no_cpu:
         threads, res = cpu_baseline(kv, pt, q[0], ctx)

@@ -134,61 +134,95 @@ __global__ __launch_bounds__(256) void append_q8_0_kernel(AppendParams p) {
 // host), with cosf / sinf of theta_i.  Q rotates in place; K rotates on its
 // way into the cache (converted as the append converts); V is appended raw.
 // A token with seq < 0 or pos < 0 is skipped entirely (Q untouched).
+// Each thread's first Q pairs and K/V unit, and its unit's page-table entry,
+// are loaded before the cos/sin table is built, so a one-token call's memory
+// waits overlap the table's math.
 constexpr int kMaxHalfDim = 64;
+constexpr int kRopeQPairs = 8;  // Q pairs per thread loaded ahead (32 heads x 64 pairs / 256)
 template <int KVT>
 __global__ __launch_bounds__(256) void rope_append_kernel(AppendParams p, float *q, int n_head,
                                                           float theta_scale) {
+    constexpr int E = KVT == SFA_KV_F16 ? 8 : kQK;  // elements per K/V unit of work
     __shared__ float cs[kMaxHalfDim][2];
     const int tok = blockIdx.x;
     const int ps = p.pos[tok];
-    if (ps < 0 || p.seq[tok] < 0) return;  // workgroup-uniform: before any barrier
+    const bool valid = ps >= 0 && p.seq[tok] >= 0;  // workgroup-uniform
+    const int tid = threadIdx.x;
     const int half = p.head_dim / 2;
-    if ((int)threadIdx.x < half) {
+    const int n_qp = q != nullptr ? n_head * half : 0;
+    const int units = p.head_dim / E;
+    const int n_units = 2 * p.n_head_kv * units;
+
+    float2 qv[kRopeQPairs];
+    float2 *qrow = q != nullptr ? reinterpret_cast<float2 *>(q + (int64_t)tok * n_head * p.head_dim) : nullptr;
+#pragma unroll
+    for (int j = 0; j < kRopeQPairs; ++j) {
+        const int idx = tid + j * (int)blockDim.x;
+        if (idx < n_qp) qv[j] = qrow[idx];
+    }
+    float x[E];
+    const bool has_unit = tid < n_units;
+    int which = 0, kvh = 0, u = 0;
+    if (has_unit) {
+        which = tid / (p.n_head_kv * units);
+        const int r = tid % (p.n_head_kv * units);
+        kvh = r / units;
+        u = r % units;
+        load_f32<E>((which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + E * u, x);
+    }
+    // the unit's destination row (a page-table read) while the loads fly
+    uint8_t *dst0 = valid && has_unit ? row_ptr(p, which, tok, kvh) : nullptr;
+
+    if (valid && tid < half) {
         float theta = (float)ps;
-        for (int j = 0; j < (int)threadIdx.x; ++j) theta *= theta_scale;
-        cs[threadIdx.x][0] = cosf(theta);
-        cs[threadIdx.x][1] = sinf(theta);
+        for (int j = 0; j < tid; ++j) theta *= theta_scale;
+        float sn, c;
+        sincosf(theta, &sn, &c);  // one argument reduction for both
+        cs[tid][0] = c;
+        cs[tid][1] = sn;
     }
     __syncthreads();
-    auto rot = [&](float (&x)[2], int i) {
-        const float c = cs[i][0], s = cs[i][1];
-        const float x0 = x[0], x1 = x[1];
-        x[0] = x0 * c - x1 * s;
-        x[1] = x0 * s + x1 * c;
+    if (!valid) return;  // after the barrier every thread of the workgroup reaches
+    auto rot = [&](float &x0, float &x1, int i) {
+        const float c = cs[i][0], sn = cs[i][1];
+        const float a0 = x0, a1 = x1;
+        x0 = a0 * c - a1 * sn;
+        x1 = a0 * sn + a1 * c;
     };
-    if (q != nullptr) {
-        for (int idx = threadIdx.x; idx < n_head * half; idx += blockDim.x) {
-            const int h = idx / half, i = idx % half;
-            float *r = q + ((int64_t)tok * n_head + h) * p.head_dim + 2 * i;
-            float x[2] = {r[0], r[1]};
-            rot(x, i);
-            r[0] = x[0];
-            r[1] = x[1];
+    // Q: pair idx of the token's row is head idx / half, pair idx % half
+#pragma unroll
+    for (int j = 0; j < kRopeQPairs; ++j) {
+        const int idx = tid + j * (int)blockDim.x;
+        if (idx < n_qp) {
+            float2 v = qv[j];
+            rot(v.x, v.y, idx % half);
+            qrow[idx] = v;
         }
     }
-    constexpr int E = KVT == SFA_KV_F16 ? 8 : kQK;  // elements per unit of work
-    const int units = p.head_dim / E;
-    for (int idx = threadIdx.x; idx < 2 * p.n_head_kv * units; idx += blockDim.x) {
-        const int which = idx / (p.n_head_kv * units);
-        const int r = idx % (p.n_head_kv * units);
-        const int kvh = r / units, u = r % units;
-        uint8_t *dst = row_ptr(p, which, tok, kvh);
-        if (dst == nullptr) continue;
-        float x[E];
-        load_f32<E>((which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + E * u, x);
-        if (which == 0) {
+    for (int idx = tid + kRopeQPairs * (int)blockDim.x; idx < n_qp; idx += blockDim.x) {
+        float2 v = qrow[idx];
+        rot(v.x, v.y, idx % half);
+        qrow[idx] = v;
+    }
+    auto put = [&](uint8_t *dst, int w, int un, float (&xs)[E]) {
+        if (dst == nullptr) return;
+        if (w == 0) {
 #pragma unroll
-            for (int j = 0; j < E; j += 2) {
-                float pr[2] = {x[j], x[j + 1]};
-                rot(pr, (E * u + j) / 2);
-                x[j] = pr[0];
-                x[j + 1] = pr[1];
-            }
+            for (int j = 0; j < E; j += 2) rot(xs[j], xs[j + 1], (E * un + j) / 2);
         }
         if constexpr (KVT == SFA_KV_F16)
-            store_f16x8(dst + 16 * u, x);
+            store_f16x8(dst + 16 * un, xs);
         else
-            store_q8_block(dst + kQ8Bytes * u, x);
+            store_q8_block(dst + kQ8Bytes * un, xs);
+    };
+    if (has_unit) put(dst0, which, u, x);
+    for (int idx = tid + (int)blockDim.x; idx < n_units; idx += blockDim.x) {
+        const int w = idx / (p.n_head_kv * units);
+        const int r = idx % (p.n_head_kv * units);
+        const int h = r / units, un = r % units;
+        float xs[E];
+        load_f32<E>((w ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + h) * p.head_dim + E * un, xs);
+        put(row_ptr(p, w, tok, h), w, un, xs);
     }
 }
 
