@@ -477,9 +477,10 @@ def rope_bench(torch, steps: int, seed: int):
         "workload": "fused RoPE (base 1e6) of Q [2048,32,128] and K [2048,8,128] + append of K, V "
                     "into an f16 paged cache at positions 2048..4095, 8 layers with distinct caches",
         "us_per_layer_chunk": round(us, 3),
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "rope_append_kernel<f16>", "bytes_per_launch": alg},
+        "roofline": with_traffic({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                                  "kernel": "rope_append_kernel<f16>", "bytes_per_launch": alg},
+                                 "rope_append_2048"),
     }
     del kv, qs, ks, vs
     torch.cuda.empty_cache()
