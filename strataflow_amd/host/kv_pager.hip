@@ -271,7 +271,13 @@ SFA_API int sfa_pager_begin(sfa_pager *p, const int32_t *n_tok, void *stream) {
         return SFA_ERR_OUT_OF_MEMORY;
     }
     p->step_open = true;
-    return p->apply(actions, as_stream(stream));
+    try {
+        return p->apply(actions, as_stream(stream));
+    } catch (const std::bad_alloc &) {  // no exception leaves the C ABI
+        return SFA_ERR_OUT_OF_MEMORY;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
 }
 
 SFA_API int sfa_pager_append(sfa_pager *p, int32_t layer, const float *k, const float *v,
@@ -331,9 +337,13 @@ SFA_API int sfa_pager_reset(sfa_pager *p, int32_t seq, void *stream) {
     p->step_tokens = 0;
     p->step_open = false;
     // the table slots of the released pages go back to -1
-    std::vector<std::pair<int32_t, int32_t>> edits;
-    for (int lp = 0; lp < p->max_pages; ++lp) edits.emplace_back(seq * p->max_pages + lp, -1);
-    return p->launch_updates(edits, as_stream(stream));
+    try {
+        std::vector<std::pair<int32_t, int32_t>> edits;
+        for (int lp = 0; lp < p->max_pages; ++lp) edits.emplace_back(seq * p->max_pages + lp, -1);
+        return p->launch_updates(edits, as_stream(stream));
+    } catch (const std::bad_alloc &) {  // no exception leaves the C ABI
+        return SFA_ERR_OUT_OF_MEMORY;
+    }
 }
 
 SFA_API int sfa_pager_stats_get(const sfa_pager *p, sfa_pager_stats *out) {
