@@ -44,16 +44,18 @@ struct DecodeParams {
     int max_pages;
     const int32_t *seq_len;
     const int32_t *kv_lo;
-    int n_splits;         // splits per (sequence, kv head)
     int n_seq;            // B
-    int split_row;        // B * n_splits rounded up to a multiple of 8
-    int tiles_per_split;  // minimum tiles per split (host heuristic)
+    int split_row;        // workgroup slots per kv head (a multiple of 8)
+    int guess_splits;     // the host's guess of splits per sequence (all at max_seq_len)
+    int guess_tiles;      // and of its tiles; the device plan decides
+    int one_split;        // 1: no merge pass runs (one sequence, guessed one split)
     float scale_log2;     // scale * log2(e)
-    float *part;          // [B][Hkv][n_splits][G][HD + 4]
+    float *part;          // [Hkv][split_row][G][HD + 4]: one (o, m, l) record per slot
 };
 
 constexpr int kDecodeWaves = 4;
 constexpr int kMaxSplits = 256;  // splits per (sequence, kv head)
+constexpr int kMaxPlanTiles = 1 << 30;  // bound on the tiles of one call (all sequences)
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold: P <= 2^8
 // merge kernel block: one thread per dim, at least one full wave
 template <int HD>
@@ -75,44 +77,178 @@ __device__ inline float head_val(const float (&arr)[G], int i, int hh) {
     }
 }
 
-// Workgroup -> (split, kv head, sequence).  The grid is 1-D with rows of
-// `split_row` = B * n_splits rounded up to a multiple of 8; workgroup L serves
-// kv head L / split_row and (sequence, split) L % split_row.  Workgroups go to
-// the eight XCDs round-robin (XCD = L % 8), so every kv head of one (sequence,
-// split) lands on the same XCD and shares its L2: Q8_0 rows (136 bytes) of
-// neighbouring kv heads share cache lines.  Returns false for padding slots.
-__device__ inline bool split_coords(const DecodeParams &p, int &split, int &kvh, int &b) {
-    const int L = blockIdx.x;
-    kvh = L / p.split_row;
-    const int j = L - kvh * p.split_row;
-    b = j / p.n_splits;
-    split = j - b * p.n_splits;
-    return b < p.n_seq;
+// ---- split plan --------------------------------------------------------------
+// Each kv head owns a row of `split_row` workgroup slots (XCD = L % 8 and
+// split_row % 8 == 0, so every kv head of one slot shares an XCD and its L2:
+// Q8_0 rows of neighbouring kv heads share cache lines).  The slots are dealt
+// out to the sequences in proportion to their active tiles: with T the sum of
+// the sequences' tiles and Z the number of sequences with any, sequence b of
+// n_b tiles takes 1 + floor((split_row - Z) * n_b / T) consecutive slots (at
+// most one per kDecodeWaves tiles, at most kMaxSplits), so the shares never
+// exceed the row and a short sequence in a batch does not leave slots idle
+// that a long one could use.  Inside a sequence the tiles are spread evenly:
+// splits differ by at most one tile.  The plan is computed on the device from
+// seq_len / kv_lo (device arrays), identically by every workgroup and by the
+// merge pass; the host only guesses it (every sequence at max_seq_len, from
+// position 0) so the first tile can be fetched before seq_len arrives.
+
+// Tiles of a sequence: 32-aligned absolute position blocks [32t, 32t+32)
+// intersecting [lo, n_kv).
+struct SeqGeom {
+    int lo, n_kv, t0, n_tiles;
+};
+__host__ __device__ inline SeqGeom seq_geom(int n_kv_raw, int lo_raw, int cap) {
+    SeqGeom g;
+    g.n_kv = n_kv_raw > cap ? cap : n_kv_raw;
+    g.lo = lo_raw < 0 ? 0 : lo_raw;
+    if (g.n_kv <= g.lo) {
+        g.t0 = 0;
+        g.n_tiles = 0;
+    } else {
+        g.t0 = g.lo / kTile;
+        g.n_tiles = (g.n_kv + kTile - 1) / kTile - g.t0;
+    }
+    return g;
 }
 
-// Active tile range of sequence b: tiles are 32-aligned absolute position
-// blocks [32t, 32t+32) intersecting [lo, n_kv).
-__device__ inline void seq_tiles_from(const DecodeParams &p, int n_kv_raw, int lo_raw, int &lo,
-                                      int &n_kv, int &t0, int &n_tiles, int &tps, int &n_active) {
-    n_kv = n_kv_raw;
-    const int cap = p.max_pages * p.page_size;
-    if (n_kv > cap) n_kv = cap;
-    lo = lo_raw;
-    if (lo < 0) lo = 0;
-    if (n_kv <= lo) {
-        t0 = 0; n_tiles = 0; tps = 1; n_active = 0;
-        return;
-    }
-    t0 = lo / kTile;
-    n_tiles = (n_kv + kTile - 1) / kTile - t0;
-    tps = p.tiles_per_split;
-    const int need = (n_tiles + p.n_splits - 1) / p.n_splits;
-    if (tps < need) tps = need;
-    n_active = (n_tiles + tps - 1) / tps;
+__host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+__host__ inline long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+
+// Splits of a sequence with n tiles, given `avail` slots to share beyond one
+// per non-empty sequence and T tiles in all (T >= n).
+__host__ __device__ inline int splits_of(int n, int avail, int T) {
+    if (n <= 0) return 0;
+    const unsigned long long prod = (unsigned long long)avail * (unsigned)n;
+    const int share = prod <= 0xffffffffull ? (int)((unsigned)prod / (unsigned)T)
+                                            : (int)(prod / (unsigned long long)T);
+    int s = 1 + share;
+    const int most = ceil_div(n, kDecodeWaves);
+    if (s > most) s = most;
+    if (s > kMaxSplits) s = kMaxSplits;
+    return s;
 }
-__device__ inline void seq_tiles(const DecodeParams &p, int b, int &lo, int &n_kv, int &t0,
-                                 int &n_tiles, int &tps, int &n_active) {
-    seq_tiles_from(p, p.seq_len[b], p.kv_lo ? p.kv_lo[b] : 0, lo, n_kv, t0, n_tiles, tps, n_active);
+
+// Tiles [lo, hi) of split s of n_s splits over n tiles from t0: the first
+// n % n_s splits take one tile more.
+__host__ __device__ inline void split_tiles(int t0, int n, int n_s, int s, int &lo, int &hi) {
+    const int q = n / n_s, r = n - q * n_s;
+    lo = t0 + s * q + (s < r ? s : r);
+    hi = lo + q + (s < r ? 1 : 0);
+}
+
+// Wave-wide integer sum (every lane gets the result) and inclusive prefix
+// sum, on DPP: butterflies or shifts inside each 16-lane row, then the rows
+// combined (readlanes for the sum; row_bcast:15 / row_bcast:31 for the scan,
+// as the atomic-optimizer scan of the AMDGPU backend does).
+template <int CTRL>
+__device__ inline int dpp_i(int x) {
+    return __builtin_amdgcn_mov_dpp(x, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL, int ROWS>
+__device__ inline int dpp_i0(int x) {  // source lanes outside the row read 0
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xf, true);
+}
+__device__ inline int lane_sum_i(int x) {
+    x += dpp_i<0xB1>(x);
+    x += dpp_i<0x4E>(x);
+    x += dpp_i<0x141>(x);
+    x += dpp_i<0x140>(x);
+    return (__builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16)) +
+           (__builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48));
+}
+__device__ inline int lane_scan_i(int x) {
+    x += dpp_i0<0x111, 0xf>(x);  // row_shr:1
+    x += dpp_i0<0x112, 0xf>(x);  // row_shr:2
+    x += dpp_i0<0x114, 0xf>(x);  // row_shr:4
+    x += dpp_i0<0x118, 0xf>(x);  // row_shr:8
+    x += dpp_i0<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+    x += dpp_i0<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+
+// The plan as one slot or one sequence sees it.
+struct SlotPlan {
+    int b;       // sequence
+    int split;   // split index within the sequence
+    int n_b;     // splits of the sequence
+    int rec0;    // its first slot in the row
+    SeqGeom g;   // the sequence's tiles
+};
+
+// Per-lane raw inputs of the plan, issued early in a kernel: lane l holds
+// sequence l (2 <= B <= 64); for a single sequence every lane holds it.
+struct PlanRaw {
+    int n_kv, lo;
+};
+__device__ inline PlanRaw plan_load(const DecodeParams &p, int lane) {
+    PlanRaw r{0, 0};
+    if (p.n_seq == 1) {
+        r.n_kv = p.seq_len[0];
+        r.lo = p.kv_lo ? p.kv_lo[0] : 0;
+    } else if (p.n_seq <= kWave && lane < p.n_seq) {
+        r.n_kv = p.seq_len[lane];
+        r.lo = p.kv_lo ? p.kv_lo[lane] : 0;
+    }
+    return r;
+}
+
+// Sequence b = -1 asks for the owner of row slot j (false: the slot is idle);
+// b >= 0 asks for sequence b's splits and first slot (the merge pass).  Every
+// lane of the wave must be active.  2 <= B <= 64: lane l computes sequence l;
+// larger batches walk the sequences wave-uniformly (slow path).
+__device__ inline bool plan(const DecodeParams &p, const PlanRaw &raw, int j, int b, int lane, SlotPlan &sp) {
+    const int cap = p.max_pages * p.page_size;
+    const int row = p.split_row;
+    if (p.n_seq == 1) {
+        sp.g = seq_geom(raw.n_kv, raw.lo, cap);
+        sp.b = 0;
+        sp.n_b = splits_of(sp.g.n_tiles, p.one_split ? 0 : row - 1, sp.g.n_tiles);
+        sp.rec0 = 0;
+        sp.split = b < 0 ? j : 0;
+        return b >= 0 || j < sp.n_b;
+    }
+    if (p.n_seq <= kWave) {
+        const SeqGeom g = lane < p.n_seq ? seq_geom(raw.n_kv, raw.lo, cap) : SeqGeom{0, 0, 0, 0};
+        const int T = lane_sum_i(g.n_tiles);
+        const int Z = __popcll(__ballot(g.n_tiles > 0));
+        const int n_lane = splits_of(g.n_tiles, row - Z, T);
+        const int pre_lane = lane_scan_i(n_lane) - n_lane;  // exclusive prefix over the lanes
+        if (b < 0) {
+            const unsigned long long m = __ballot(n_lane > 0 && pre_lane <= j && j < pre_lane + n_lane);
+            if (m == 0) return false;
+            b = __builtin_ctzll(m);
+        }
+        sp.b = b;
+        sp.n_b = __shfl(n_lane, b, kWave);
+        sp.rec0 = __shfl(pre_lane, b, kWave);
+        sp.g.lo = __shfl(g.lo, b, kWave);
+        sp.g.n_kv = __shfl(g.n_kv, b, kWave);
+        sp.g.t0 = __shfl(g.t0, b, kWave);
+        sp.g.n_tiles = __shfl(g.n_tiles, b, kWave);
+        sp.split = j - sp.rec0;
+        return true;
+    }
+    int T = 0, Z = 0;
+    for (int bb = 0; bb < p.n_seq; ++bb) {
+        const SeqGeom gb = seq_geom(p.seq_len[bb], p.kv_lo ? p.kv_lo[bb] : 0, cap);
+        T += gb.n_tiles;
+        Z += gb.n_tiles > 0;
+    }
+    int pre = 0;
+    for (int bb = 0; bb < p.n_seq; ++bb) {
+        const SeqGeom gb = seq_geom(p.seq_len[bb], p.kv_lo ? p.kv_lo[bb] : 0, cap);
+        const int nb = splits_of(gb.n_tiles, row - Z, T);
+        if (b >= 0 ? bb == b : j < pre + nb) {
+            sp.b = bb;
+            sp.n_b = nb;
+            sp.rec0 = pre;
+            sp.g = gb;
+            sp.split = j - pre;
+            return true;
+        }
+        pre += nb;
+    }
+    return false;
 }
 
 // Workgroup epilogue of a split: the four waves' (m, l, O^T) for the g heads
@@ -123,7 +259,7 @@ __device__ inline void seq_tiles(const DecodeParams &p, int b, int &lo, int &n_k
 template <int HD, int G>
 __device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run, float l_run,
                                       float (*lds_m)[G], float (*lds_l)[G], float (*lds_o)[G][HD],
-                                      const DecodeParams &p, int b, int kvh, int split, int n_active,
+                                      const DecodeParams &p, int kvh, int slot, int n_b,
                                       float *out_b, int wave, int n, int hh) {
     constexpr int DB = HD / 32;
     if (n < G) {
@@ -140,8 +276,7 @@ __device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run,
         }
     }
     __syncthreads();
-    const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
-    float *part = p.part + (head_base * p.n_splits + split) * G * (HD + 4);
+    float *part = p.part + ((int64_t)kvh * p.split_row + slot) * G * (HD + 4);
     for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
         const int g = idx / HD, d = idx % HD;
         float M = -INFINITY;
@@ -155,7 +290,7 @@ __device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run,
             L += lds_l[w][g] * wt;
             O += lds_o[w][g][d] * wt;
         }
-        if (n_active == 1) {
+        if (n_b == 1) {
             out_b[g * HD + d] = L > 0.0f ? O / L : 0.0f;
         } else {
             part[g * (HD + 4) + d] = O;
@@ -184,13 +319,19 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 lds_q[G * HD];
     __shared__ float lds_o[kDecodeWaves][G][HD];
 
-    int split, kvh, b;
-    if (!split_coords(p, split, kvh, b)) return;
+    // slot j of kv head kvh's row; (b_g, split_g) is the host's guess of its
+    // sequence and split, used to start the first tile's loads before the
+    // plan (which needs seq_len) is known
+    const int kvh = (int)blockIdx.x / p.split_row;
+    const int slot = (int)blockIdx.x - kvh * p.split_row;
+    int b_g = slot / p.guess_splits;
+    if (b_g >= p.n_seq) b_g = p.n_seq - 1;
+    const int split_g = slot - b_g * p.guess_splits;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int n = lane & 31;   // MFMA column (head replica) / A-operand row
     const int hh = lane >> 5;  // k half
-    const int32_t *pt = p.page_table + (int64_t)b * p.max_pages;
+    const int32_t *pt = p.page_table + (int64_t)b_g * p.max_pages;
 
     const int Hkv = p.n_head_kv;
     const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
@@ -231,10 +372,11 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     // first tile, as the host plan places it (kv_lo 0, seq_len within the
     // plan), is fetched before seq_len is known and re-issued below if the
     // guess was wrong.
-    const int t_guess = __builtin_amdgcn_readfirstlane(split * p.tiles_per_split + wave);
+    int t_guess, t_guess_hi;
+    split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
+    t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave);
     pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
-    const int n_kv_raw = p.seq_len[b];
-    const int lo_raw = p.kv_lo ? p.kv_lo[b] : 0;
+    const PlanRaw raw = plan_load(p, lane);
     // Q of the g heads rounded to f16 (the F16 vec_dot_type conversion ggml
     // applies to src1), staged once per workgroup in LDS; the Q^T operand of
     // column n (head n % g, dims 16c + 8hh .. +8) is re-read per tile, which
@@ -242,13 +384,35 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     static_assert(G * HD / 8 <= 256, "one Q chunk per thread");
     const bool q_thread = threadIdx.x < G * HD / 8;
     floatx4 qx0 = floatx4{}, qx1 = floatx4{};
-    if (q_thread) {
-        const floatx4 *qr = reinterpret_cast<const floatx4 *>(
-            p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD);
-        qx0 = qr[2 * threadIdx.x];
-        qx1 = qr[2 * threadIdx.x + 1];
-    }
+    auto load_q = [&](int bq) {
+        if (q_thread) {
+            const floatx4 *qr = reinterpret_cast<const floatx4 *>(
+                p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
+            qx0 = qr[2 * threadIdx.x];
+            qx1 = qr[2 * threadIdx.x + 1];
+        }
+    };
+    load_q(b_g);
     bool tile_ok = issue(t_guess);
+
+    SlotPlan sp;
+    if (!plan(p, raw, slot, -1, lane, sp)) {
+        // an idle slot; the merge pass writes the output of a sequence
+        // without tiles, or, for one sequence, the slot that would own it
+        if (p.n_seq == 1 && slot == 0 && sp.n_b == 0) {
+            float *out0 = p.out + (int64_t)kvh * G * HD;
+            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out0[i] = 0.0f;
+        }
+        return;
+    }
+    const int b = sp.b;
+    int tile_lo, tile_hi;
+    split_tiles(sp.g.t0, sp.g.n_tiles, sp.n_b, sp.split, tile_lo, tile_hi);
+    if (b != b_g) {  // a wrong guess: this slot serves another sequence
+        pt = p.page_table + (int64_t)b * p.max_pages;
+        pages.load(pt, p.max_pages, tile_lo * kTile / p.page_size, lane);
+        load_q(b);
+    }
     if (q_thread) {
         half8 h;
         h[0] = (_Float16)qx0[0]; h[1] = (_Float16)qx0[1]; h[2] = (_Float16)qx0[2]; h[3] = (_Float16)qx0[3];
@@ -256,20 +420,10 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
         reinterpret_cast<half8 *>(lds_q)[threadIdx.x] = h;
     }
 
-    int lo, n_kv, t0, n_tiles, tps, n_active;
-    seq_tiles_from(p, n_kv_raw, lo_raw, lo, n_kv, t0, n_tiles, tps, n_active);
+    const int lo = sp.g.lo, n_kv = sp.g.n_kv;
     float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
-    if (split >= n_active) {
-        if (split == 0 && n_active == 0) {
-            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out_b[i] = 0.0f;
-        }
-        return;
-    }
-    const int tile_lo = t0 + split * tps;
-    int tile_hi = tile_lo + tps;
-    if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
     int t = tile_lo + wave_u;
-    if (t != t_guess) tile_ok = t < tile_hi ? issue(t) : false;
+    if (t != t_guess || b != b_g) tile_ok = t < tile_hi ? issue(t) : false;
     __syncthreads();
     const half8 *qrow = reinterpret_cast<const half8 *>(lds_q) + (n % G) * (HD / 8) + hh;
 
@@ -382,7 +536,7 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     }
 
     l_run += xor32(l_run);
-    split_epilogue<HD, G>(o, m_run, l_run, lds_m, lds_l, lds_o, p, b, kvh, split, n_active, out_b,
+    split_epilogue<HD, G>(o, m_run, l_run, lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b,
                           wave, n, hh);
 }
 
@@ -417,13 +571,17 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     __shared__ float lds_l[kDecodeWaves][G];
     __shared__ float lds_o[kDecodeWaves][G][HD];
 
-    int split, kvh, b;
-    if (!split_coords(p, split, kvh, b)) return;
+    // slot of kv head kvh's row and the host's guess of its sequence / split
+    const int kvh = (int)blockIdx.x / p.split_row;
+    const int slot = (int)blockIdx.x - kvh * p.split_row;
+    int b_g = slot / p.guess_splits;
+    if (b_g >= p.n_seq) b_g = p.n_seq - 1;
+    const int split_g = slot - b_g * p.guess_splits;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int n = lane & 31;   // tile position (QK) / MFMA column (PV)
     const int hh = lane >> 5;
-    const int32_t *pt = p.page_table + (int64_t)b * p.max_pages;
+    const int32_t *pt = p.page_table + (int64_t)b_g * p.max_pages;
     const int Hkv = p.n_head_kv;
     const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
     uint8_t *vt = lds_v[wave];
@@ -486,22 +644,43 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
 
     // Prologue order as in the f16 kernel: page-id window, seq_len / kv_lo
     // and the lane's Q values are issued before the first tile's K/V burst.
-    const int t_guess = __builtin_amdgcn_readfirstlane(split * p.tiles_per_split + wave);
+    int t_guess, t_guess_hi;
+    split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
+    t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave);
     pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
-    const int n_kv_raw = p.seq_len[b];
-    const int lo_raw = p.kv_lo ? p.kv_lo[b] : 0;
+    const PlanRaw raw = plan_load(p, lane);
     const int hq = n % G;
     floatx4 qraw[NB][4];
-    {
-        const float *qr = p.q + ((int64_t)b * p.n_head + (int64_t)kvh * G + hq) * HD;
+    auto load_q = [&](int bq) {
+        const float *qr = p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G + hq) * HD;
 #pragma unroll
         for (int c = 0; c < NB; ++c)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 qraw[c][j] = reinterpret_cast<const floatx4 *>(qr + 32 * c + 16 * hh)[j];
-    }
+    };
+    load_q(b_g);
     Raw ra, rb;
     bool ok_a = issue(t_guess, ra);
+
+    SlotPlan sp;
+    if (!plan(p, raw, slot, -1, lane, sp)) {
+        // an idle slot; the merge pass writes the output of a sequence
+        // without tiles, or, for one sequence, the slot that would own it
+        if (p.n_seq == 1 && slot == 0 && sp.n_b == 0) {
+            float *out0 = p.out + (int64_t)kvh * G * HD;
+            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out0[i] = 0.0f;
+        }
+        return;
+    }
+    const int b = sp.b;
+    int tile_lo, tile_hi;
+    split_tiles(sp.g.t0, sp.g.n_tiles, sp.n_b, sp.split, tile_lo, tile_hi);
+    if (b != b_g) {  // a wrong guess: this slot serves another sequence
+        pt = p.page_table + (int64_t)b * p.max_pages;
+        pages.load(pt, p.max_pages, tile_lo * kTile / p.page_size, lane);
+        load_q(b);
+    }
 
     // Q8_0 of Q, the MFMA A operand: lane row m = n is head n % G, block c,
     // elements 16hh .. 16hh+15; staged in LDS (read per tile, which keeps 16
@@ -532,23 +711,13 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
         }
     }
 
-    int lo, n_kv, t0, n_tiles, tps, n_active;
-    seq_tiles_from(p, n_kv_raw, lo_raw, lo, n_kv, t0, n_tiles, tps, n_active);
+    const int lo = sp.g.lo, n_kv = sp.g.n_kv;
     float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
-    if (split >= n_active) {
-        if (split == 0 && n_active == 0) {
-            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out_b[i] = 0.0f;
-        }
-        return;
-    }
     __syncthreads();  // lds_qa, lds_dq (d_q of the heads of output rows i = 0..3,
                       // i.e. rows 4hh + i, head (4hh + i) % G, read per tile)
 
-    const int tile_lo = t0 + split * tps;
-    int tile_hi = tile_lo + tps;
-    if (tile_hi > t0 + n_tiles) tile_hi = t0 + n_tiles;
     int t = tile_lo + wave_u;
-    if (t != t_guess) ok_a = t < tile_hi ? issue(t, ra) : false;
+    if (t != t_guess || b != b_g) ok_a = t < tile_hi ? issue(t, ra) : false;
 
     floatx16 o[DB];
 #pragma unroll
@@ -753,17 +922,19 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
 #pragma unroll
     for (int h = 1; h < G; ++h)
         if (n % G == h) { m_col = m_run[h]; l_col = Lh[h]; }
-    split_epilogue<HD, G>(o, m_col, l_col, lds_m, lds_l, lds_o, p, b, kvh, split, n_active, out_b,
+    split_epilogue<HD, G>(o, m_col, l_col, lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b,
                           wave, n, hh);
 }
 
 // Second pass: out = sum_s o_s * 2^(m_s - M) / sum_s l_s * 2^(m_s - M) over
 // the active splits of each (sequence, kv head), M the largest m_s.  One
-// workgroup per (b, kv head, group head), one thread per dim.  Every load of
-// the first 64 splits (the lane-parallel (m, l) of all splits and this dim's
-// o_s) is issued before seq_len is read, so the kernel waits on memory once
-// for up to 64 splits; split indices past n_splits are clamped (the loads
-// stay inside the workspace) and their weights are zero.  The code is
+// workgroup per (b, kv head, group head), one thread per dim.  For one
+// sequence every load of the first 64 splits (the lane-parallel (m, l) of all
+// splits and this dim's o_s) is issued before seq_len is read, so the kernel
+// waits on memory once; in a batch the plan (from every seq_len) first places
+// the sequence's records in the row.  Split indices past the sequence's are
+// clamped (the loads stay inside the workspace) and their weights are zero.
+// A batch sequence without tiles gets a zero output here.  The code is
 // branch-free straight-line work: the pass is latency-bound and each taken
 // branch or instruction-cache miss adds to it.
 template <int HD, int G>
@@ -776,10 +947,19 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int d = tid < HD ? tid : HD - 1;  // threads past HD (HD < 64) only load (m, l)
-    const int64_t head_base = (int64_t)b * p.n_head_kv + kvh;
-    const float *pg = p.part + head_base * p.n_splits * G * (HD + 4) + g * (HD + 4);
     const int sstride = G * (HD + 4);
-    const int S = p.n_splits;
+    const float *row0 = p.part + (int64_t)kvh * p.split_row * sstride + g * (HD + 4);
+    // one sequence owns the row from slot 0, so its records are fetched
+    // before seq_len is read; in a batch the plan places them first
+    const PlanRaw raw = plan_load(p, lane);
+    SlotPlan sp;
+    int rec0 = 0, S = p.split_row;
+    if (p.n_seq > 1) {
+        plan(p, raw, 0, b, lane, sp);
+        rec0 = sp.rec0;
+        S = sp.n_b > 0 ? sp.n_b : 1;
+    }
+    const float *pg = row0 + (int64_t)rec0 * sstride;
 
     float o[CH];
     auto load_round = [&](int s0) {
@@ -797,9 +977,15 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
         mv[r] = pg[s * sstride + HD];
         lv[r] = pg[s * sstride + HD + 1];
     }
-    int lo, n_kv, t0, n_tiles, tps, n_active;
-    seq_tiles(p, b, lo, n_kv, t0, n_tiles, tps, n_active);
-    if (n_active <= 1) return;  // one split: written by the split pass
+    if (p.n_seq == 1) plan(p, raw, 0, 0, lane, sp);
+    const int n_active = sp.n_b;
+    if (n_active <= 1) {
+        // one split: written by the split pass; none (a batch sequence with
+        // no tiles): the output is zero
+        if (n_active == 0 && p.n_seq > 1 && tid < HD)
+            p.out[((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD + tid] = 0.0f;
+        return;
+    }
 
     float mx = -INFINITY;
 #pragma unroll
@@ -838,30 +1024,36 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
 // ---- host side -------------------------------------------------------------
 
 struct SplitPlan {
-    int n_splits;
-    int tiles_per_split;
+    int split_row;     // slots per kv head
+    int guess_splits;  // splits per sequence if every sequence had max_seq_len from 0
+    int guess_tiles;
 };
 
-SplitPlan plan_splits(int B, int Hkv, int max_seq_len) {
-    const int tiles = (max_seq_len + kTile - 1) / kTile;
-    const int heads = B * Hkv;
-    // one round of workgroups: two 4-wave workgroups per CU (two waves per
-    // SIMD at these register footprints) over 256 CUs; longer contexts give
-    // each wave more tiles, whose loads the tile loop prefetches one ahead
+// About 512 workgroups (two 4-wave workgroups per CU at these register
+// footprints, over 256 CUs): the row of each kv head gets 512 / Hkv slots, at
+// most kMaxSplits, no more than the batch could use (every sequence's widest
+// span of max_seq_len positions, which covers one tile more when a window start
+// is not tile-aligned, cut into kDecodeWaves-tile splits), at least B, rounded
+// up to a multiple of 8.  The device plan deals the slots out by length.
+SplitPlan plan_splits(int B, int Hkv, int max_seq_len, bool windowed) {
     const int wg_target = 512;
-    int S = (wg_target + heads - 1) / heads;
-    if (S < 1) S = 1;
-    if (S > kMaxSplits) S = kMaxSplits;
-    int tps = (tiles + S - 1) / S;
-    if (tps < kDecodeWaves) tps = kDecodeWaves;
-    S = (tiles + tps - 1) / tps;
-    if (S < 1) S = 1;
-    return SplitPlan{S, tps};
+    const int tiles = ceil_div(max_seq_len, kTile);
+    const int span_tiles = windowed ? ceil_div(max_seq_len - 1, kTile) + 1 : tiles;
+    int row = (wg_target + Hkv - 1) / Hkv;
+    if (row > kMaxSplits) row = kMaxSplits;
+    const long long most = (long long)B * ceil_div(span_tiles, kDecodeWaves);
+    if (row > most) row = (int)most;
+    if (row < B) row = B;
+    row = (row + 7) / 8 * 8;
+    // the guess, with the device's rule: every sequence max_seq_len from 0
+    const int avail = row - B;
+    const int g = splits_of(tiles, avail / B, tiles);
+    return SplitPlan{row, g > 0 ? g : 1, tiles};
 }
 
 size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
-    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len);
-    return (size_t)B * Hkv * sp.n_splits * G * (HD + 4) * sizeof(float);
+    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, true);  // the larger row
+    return (size_t)Hkv * sp.split_row * G * (HD + 4) * sizeof(float);
 }
 
 // pass bit 1: split-K pass, bit 2: merge pass
@@ -876,7 +1068,7 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
             hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
         }
     }
-    if ((passes & 2) && p.n_splits > 1)
+    if ((passes & 2) && !p.one_split)
         hipLaunchKernelGGL((decode_merge_kernel<HD, G>), dim3(B * Hkv * G), dim3(kMergeThreads<HD>), 0,
                            s, p);
 }
@@ -898,11 +1090,15 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
                   int passes, hipStream_t stream) {
     const int Hkv = kv->n_head_kv, HD = kv->head_dim, G = kv->n_head / kv->n_head_kv;
     if (B <= 0 || max_seq_len <= 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
+    // the split plan sums tile counts over the batch in 32-bit integers
+    const long long cap_tiles = ceil_div((long long)max_pages * kv->page_size, (long long)kTile);
+    if ((long long)B * cap_tiles > kMaxPlanTiles)
+        return SFA_ERR_INVALID_ARGUMENT;
     if (q == nullptr || out == nullptr || page_table == nullptr || seq_len == nullptr)
         return SFA_ERR_INVALID_ARGUMENT;
     const size_t need = decode_workspace_bytes(B, Hkv, G, HD, max_seq_len);
     if (workspace == nullptr || ws_bytes < need) return SFA_ERR_INVALID_ARGUMENT;
-    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len);
+    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, kv_lo != nullptr);
 
     DecodeParams p;
     p.k_pages = static_cast<const uint8_t *>(kv->k_pages);
@@ -922,10 +1118,11 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     p.max_pages = max_pages;
     p.seq_len = seq_len;
     p.kv_lo = kv_lo;
-    p.n_splits = sp.n_splits;
     p.n_seq = B;
-    p.split_row = (B * sp.n_splits + 7) / 8 * 8;
-    p.tiles_per_split = sp.tiles_per_split;
+    p.split_row = sp.split_row;
+    p.guess_splits = sp.guess_splits;
+    p.guess_tiles = sp.guess_tiles;
+    p.one_split = B == 1 && sp.guess_splits == 1;
     p.scale_log2 = scale * 1.4426950408889634f;
     p.part = static_cast<float *>(workspace);
 

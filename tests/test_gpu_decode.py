@@ -214,3 +214,40 @@ def test_decode_q8_window_and_placement(gpu, oracle_mod):
     pt = c.page_table.copy(); valid = pt >= 0; pt[valid] = perm[pt[valid]]
     c.t_pt = torch.from_numpy(pt).to(gpu)
     assert np.array_equal(c.decode().view(np.uint32), base.view(np.uint32))
+
+
+@pytest.mark.parametrize("kv_type", [1, 8])
+@pytest.mark.parametrize("B", [2, 64, 65, 100])
+def test_decode_split_plan_batches(gpu, oracle_mod, kv_type, B):
+    # the split plan deals each kv head's row of workgroups out by sequence
+    # length: a lane per sequence up to 64 sequences, a sequential walk above;
+    # lengths span empty, one token, one tile and a few thousand positions,
+    # some with a window start, and max_seq_len overstates the longest span
+    rng = np.random.default_rng(100 + B + kv_type)
+    seq = rng.integers(0, 2400, B)
+    seq[0], seq[-1] = 0, 1
+    if B > 2:
+        seq[1] = 32
+        seq[B // 2] = 2400
+    lo = np.where(rng.random(B) < 0.25, rng.integers(0, 400, B), 0)
+    lo = np.minimum(lo, np.maximum(seq - 1, 0))
+    c = Case(oracle_mod, seq_lens=seq, kv_lo=lo, n_head=8, n_head_kv=2, head_dim=128,
+             kv_type=kv_type, seed=200 + B)
+    out = c.decode(max_seq_len=3000)
+    assert_close(out, c.oracle(oracle_mod.GGML), what=f"B={B} type {kv_type} vs ggml")
+    assert np.all(out[0] == 0)
+
+
+def test_decode_span_beyond_max_seq_len(gpu, oracle_mod):
+    # a span longer than max_seq_len is attended in full by longer splits
+    c = Case(oracle_mod, seq_lens=[3000, 200], seed=210)
+    out = c.decode(max_seq_len=500)
+    assert_close(out, c.oracle(oracle_mod.GGML), what="span beyond max_seq_len")
+
+
+def test_decode_one_sequence_beyond_max_seq_len(gpu, oracle_mod):
+    # one sequence, a max_seq_len that plans a single split (no merge pass):
+    # the longer span is still attended in full, by that one split
+    c = Case(oracle_mod, seq_lens=[1500], seed=211)
+    out = c.decode(max_seq_len=100)
+    assert_close(out, c.oracle(oracle_mod.GGML), what="one sequence beyond max_seq_len")
