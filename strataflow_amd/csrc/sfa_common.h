@@ -21,6 +21,10 @@ constexpr int kWave = 64;
 constexpr int kTile = 32;    // positions per wave tile in decode
 constexpr int kQK = 32;      // Q8_0 block length
 constexpr int kQ8Bytes = 34; // sizeof(block_q8_0)
+// Word 3 of a raw (unformatted, stride 0) buffer resource on gfx9-family
+// parts: data format 32 bits, no swizzle, no index stride.  num_records then
+// counts bytes and a load past it returns zeros instead of reading memory.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 // Row bytes of one (position, kv head) row for a cache type; 0 if unsupported.
 __host__ __device__ inline int row_bytes_of(int kv_type, int head_dim) {

@@ -40,6 +40,9 @@ struct PrefillParams {
 };
 
 constexpr int kPBN = 64;           // positions per prefill tile
+struct HalfPairs {
+    half2v v[4];  // the four dwords of a half8
+};
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (P <= 2^8)
 
 template <int HD, int G>
@@ -97,9 +100,15 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     const int tile1 = kv_hi / kPBN;             // inclusive
     const bool block_full = (qblk + 1) * QB <= p.T;
 
-    // cooperative tile loads into registers: chunk i*256 + tid -> row r, 16B chunk c
+    // cooperative tile loads into registers: chunk i*256 + tid -> row r =
+    // 16i + tid / CPR, 16-byte chunk c = tid % CPR.  Buffer loads: the tile's
+    // page base is a scalar resource (records end at the tile, so nothing past
+    // it is read), the lane offset a constant, row block i a scalar offset.
+    static_assert(256 % CPR == 0, "row blocks");
+    constexpr int RPI = 256 / CPR;  // rows per load instruction
     half8 kreg[LPT], vreg[LPT];
     bool page_ok = false;
+    const int lane_off = (tid / CPR) * (int)col_bytes + 16 * (tid % CPR);
     auto load = [&](int t) {
         const int pos0 = t * kPBN;
         const int lp = pos0 / p.page_size;
@@ -109,19 +118,34 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         page_ok = kb != nullptr && vb != nullptr;
         if (!page_ok) return;
         const int64_t base = (int64_t)(pos0 - lp * p.page_size) * col_bytes + (int64_t)kvh * HD * 2;
+        const int n_rec = (int)(kPBN * col_bytes);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(kb + base), 0, n_rec, kBufferRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(vb + base), 0, n_rec, kBufferRsrcWord3);
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
-            const int id = i * 256 + tid;
-            const int r = id / CPR, c = id % CPR;
-            const int64_t off = base + (int64_t)r * col_bytes + 16 * c;
-            kreg[i] = *reinterpret_cast<const half8 *>(kb + off);
-            vreg[i] = *reinterpret_cast<const half8 *>(vb + off);
+            const int soff = i * RPI * (int)col_bytes;
+            kreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off, soff, 0));
+            vreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, lane_off, soff, 0));
         }
     };
     // registers -> LDS buffer; V rows outside [lo, kv_hi] zeroed (a page's
-    // unwritten tail may hold any bytes), K rows are masked in the scores
+    // unwritten tail may hold any bytes), K rows are masked in the scores.
+    // Tiles wholly inside the range with a valid page store unmasked.
     auto store = [&](int t, int buf) {
         const int pos0 = t * kPBN;
+        const bool whole = page_ok && pos0 >= lo && pos0 + kPBN - 1 <= kv_hi;  // wave-uniform
+        if (whole) {
+#pragma unroll
+            for (int i = 0; i < LPT; ++i) {
+                const int id = i * 256 + tid;
+                const int r = id / CPR, c = id % CPR;
+                *reinterpret_cast<half8 *>(&lds_k[buf][r * KROW + 16 * (c ^ (r % CPR))]) = kreg[i];
+                *reinterpret_cast<half8 *>(&lds_v[buf][r * ROW + 16 * c]) = vreg[i];
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int id = i * 256 + tid;
@@ -215,17 +239,24 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
             m_run = mt;
         }
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        float ls = 0.0f;
         half8 pbv[2][2];
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float e = __builtin_amdgcn_exp2f(fmaf(s[pb][i], p.scale_log2, -m_use));
-                ls += e;
-                pbv[pb][i >> 3][i & 7] = (_Float16)e;
-            }
+            for (int i = 0; i < 16; ++i)
+                pbv[pb][i >> 3][i & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[pb][i], p.scale_log2, -m_use));
         }
+        // the row sum of the f16 weights the P*V product uses, two per
+        // v_dot2_f32_f16 into an f32 accumulator
+        float ls = 0.0f;
+        const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(HalfPairs, pbv[pb][kk]).v[j], ones, ls, false);
         l_run = l_run * alpha + ls;
         if (__any(alpha != 1.0f)) {
 #pragma unroll
