@@ -196,7 +196,8 @@ __device__ inline PlanRaw plan_load(const DecodeParams &p, int lane) {
 // b >= 0 asks for sequence b's splits and first slot (the merge pass).  Every
 // lane of the wave must be active.  2 <= B <= 64: lane l computes sequence l;
 // larger batches walk the sequences wave-uniformly (slow path).
-__device__ inline bool plan(const DecodeParams &p, const PlanRaw &raw, int j, int b, int lane, SlotPlan &sp) {
+__device__ inline bool plan_lanes(const DecodeParams &p, const PlanRaw &raw, int j, int b, int lane, SlotPlan &sp) {
+    sp = SlotPlan{0, 0, 0, 0, SeqGeom{0, 0, 0, 0}};
     const int cap = p.max_pages * p.page_size;
     const int row = p.split_row;
     if (p.n_seq == 1) {
@@ -249,6 +250,21 @@ __device__ inline bool plan(const DecodeParams &p, const PlanRaw &raw, int j, in
         pre += nb;
     }
     return false;
+}
+
+// The plan with every field wave-uniform (scalar registers), so the tile
+// bounds and the interior / edge tests derived from it are scalar branches.
+__device__ inline bool plan(const DecodeParams &p, const PlanRaw &raw, int j, int b, int lane, SlotPlan &sp) {
+    const bool ok = plan_lanes(p, raw, j, b, lane, sp);
+    sp.b = __builtin_amdgcn_readfirstlane(sp.b);
+    sp.split = __builtin_amdgcn_readfirstlane(sp.split);
+    sp.n_b = __builtin_amdgcn_readfirstlane(sp.n_b);
+    sp.rec0 = __builtin_amdgcn_readfirstlane(sp.rec0);
+    sp.g.lo = __builtin_amdgcn_readfirstlane(sp.g.lo);
+    sp.g.n_kv = __builtin_amdgcn_readfirstlane(sp.g.n_kv);
+    sp.g.t0 = __builtin_amdgcn_readfirstlane(sp.g.t0);
+    sp.g.n_tiles = __builtin_amdgcn_readfirstlane(sp.g.n_tiles);
+    return ok;
 }
 
 // Workgroup epilogue of a split: the four waves' (m, l, O^T) for the g heads
@@ -436,21 +452,30 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     bool first = true;
     for (; t < tile_hi; t += kDecodeWaves) {
         const int pos0 = t * kTile;
-        if (!tile_ok) {  // invalid page id: this tile contributes nothing
-            tile_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
-            continue;
-        }
+        // an invalid page id (tile_ok false) leaves the registers stale: the
+        // tile then runs fully masked and contributes nothing
+        const bool dead = !tile_ok;
         // S^T = K * Q^T
         floatx16 s0 = floatx16{};
 #pragma unroll
         for (int c = 0; c < KC; ++c) s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qrow[2 * c], s0, 0, 0, 0);
         // V tile into the wave's LDS region; rows outside [lo, n_kv) zeroed
-        // (they may hold stale bytes of a page's unused tail)
+        // (they may hold stale bytes of a page's unused tail).  Interior
+        // tiles (a scalar test) store unmasked.
+        const bool interior = !dead && pos0 >= lo && pos0 + kTile <= n_kv;
+        if (interior) {
 #pragma unroll
-        for (int i = 0; i < VIT; ++i) {
-            const int r = i * RPI + lane / CPR;
-            const bool ok = pos0 + r >= lo && pos0 + r < n_kv;
-            *reinterpret_cast<half8 *>(vt + r * VROW + 16 * (lane % CPR)) = ok ? vr[i] : half8{};
+            for (int i = 0; i < VIT; ++i) {
+                const int r = i * RPI + lane / CPR;
+                *reinterpret_cast<half8 *>(vt + r * VROW + 16 * (lane % CPR)) = vr[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < VIT; ++i) {
+                const int r = i * RPI + lane / CPR;
+                const bool ok = !dead && pos0 + r >= lo && pos0 + r < n_kv;
+                *reinterpret_cast<half8 *>(vt + r * VROW + 16 * (lane % CPR)) = ok ? vr[i] : half8{};
+            }
         }
         // registers are free: start the next tile's loads now
         const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
@@ -460,7 +485,6 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
         // max moves only when a score exceeds it by 2^8 (a wave-uniform
         // ballot), so most tiles skip the max exchange and the O rescale;
         // P <= 256 and O, l share the reference, so the result is unchanged.
-        const bool interior = pos0 >= lo && pos0 + kTile <= n_kv;
         float sv[16];
         float mt = -INFINITY;
 #pragma unroll
@@ -468,7 +492,7 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
             float v = s0[i] * p.scale_log2;
             if (!interior) {
                 const int pp = pos0 + 8 * (i >> 2) + 4 * hh + (i & 3);
-                v = (pp >= lo && pp < n_kv) ? v : -INFINITY;
+                v = (!dead && pp >= lo && pp < n_kv) ? v : -INFINITY;
             }
             sv[i] = v;
             mt = fmaxf(mt, v);
@@ -955,7 +979,7 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     SlotPlan sp;
     int rec0 = 0, S = p.split_row;
     if (p.n_seq > 1) {
-        plan(p, raw, 0, b, lane, sp);
+        plan_lanes(p, raw, 0, b, lane, sp);  // per-lane selects below; no scalar copy needed
         rec0 = sp.rec0;
         S = sp.n_b > 0 ? sp.n_b : 1;
     }
@@ -977,7 +1001,7 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
         mv[r] = pg[s * sstride + HD];
         lv[r] = pg[s * sstride + HD + 1];
     }
-    if (p.n_seq == 1) plan(p, raw, 0, 0, lane, sp);
+    if (p.n_seq == 1) plan_lanes(p, raw, 0, 0, lane, sp);
     const int n_active = sp.n_b;
     if (n_active <= 1) {
         // one split: written by the split pass; none (a batch sequence with
