@@ -21,8 +21,9 @@
  *   cache: one "column" per position = n_head_kv rows of head_dim elements
  *          (k_cache [hd, Hkv, W], engine.cpp:1264-1275).  A page is page_size
  *          consecutive columns: byte offset of (pos_in_page, kv_head) is
- *          (pos_in_page * n_head_kv + kv_head) * row_bytes.  F16 rows are head_dim
- *          IEEE halves; Q8_0 rows are head_dim/32 ggml block_q8_0 records
+ *          (pos_in_page * n_head_kv + kv_head) * row_bytes.  F32 rows are head_dim
+ *          floats (the reference's own cache type); F16 rows are head_dim IEEE
+ *          halves; Q8_0 rows are head_dim/32 ggml block_q8_0 records
  *          {fp16 d; int8 qs[32]} (34 bytes each).
  *   GQA  : query head h reads kv head h / (n_head / n_head_kv).
  *
@@ -70,7 +71,7 @@ typedef struct sfa_kv_desc {
     int32_t n_head_kv;     /* Hkv; n_head % n_head_kv == 0                      */
     int32_t head_dim;      /* 32, 64 or 128                                     */
     int32_t page_size;     /* positions per page, a multiple of 32              */
-    int32_t kv_type;       /* SFA_KV_F16 or SFA_KV_Q8_0                         */
+    int32_t kv_type;       /* SFA_KV_F32, SFA_KV_F16 or SFA_KV_Q8_0             */
     int32_t n_pages;       /* pages in k_pages / v_pages                        */
     void   *k_pages;       /* device, n_pages * sfa_page_bytes()                */
     void   *v_pages;
@@ -98,9 +99,9 @@ SFA_API int sfa_kv_desc_check(const sfa_kv_desc *kv);
 /* KV append: the ggml_cpy of Kcur/Vcur into the cache column of each token
  * (engine.cpp:1646-1656).  k, v: [n_tok][n_head_kv][head_dim] f32; token i
  * belongs to sequence seq[i] at absolute position pos[i]; its row lands in
- * page page_table[seq[i] * max_pages + pos[i] / page_size].  F16 caches round
- * to nearest even; Q8_0 caches quantise each 32-block with d = amax/127 (fp16)
- * and q = round(x / d).  The kernel writes nothing for a token whose page id
+ * page page_table[seq[i] * max_pages + pos[i] / page_size].  F32 caches store
+ * the values as they are; F16 caches round to nearest even; Q8_0 caches
+ * quantise each 32-block with d = amax/127 (fp16) and q = round(x / d).  The kernel writes nothing for a token whose page id
  * is -1 or outside its pool (it cannot report that back without a sync), so
  * callers validate host page tables with sfa_page_table_check(). */
 SFA_API int sfa_kv_append(const sfa_kv_desc *kv, const float *k, const float *v,
@@ -178,7 +179,8 @@ SFA_API int sfa_attn_decode_merge(const sfa_kv_desc *kv, const float *q, float *
  * q_pos0 .. q_pos0+T-1, whose K/V are already appended.  Token t attends kv
  * positions kv_lo .. q_pos0+t (causal -INF mask above the diagonal, the
  * llama.cpp kq_mask convention).  q: [T][n_head][head_dim] f32,
- * out: [T][n_head * head_dim] f32.  F16 caches only. */
+ * out: [T][n_head * head_dim] f32.  F32 and F16 caches (a Q8_0 cache returns
+ * SFA_ERR_UNSUPPORTED). */
 SFA_API int sfa_attn_prefill(const sfa_kv_desc *kv, const float *q, float *out,
                              const int32_t *page_table, int32_t max_pages,
                              int32_t q_pos0, int32_t T, int32_t kv_lo,

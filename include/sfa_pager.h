@@ -41,7 +41,7 @@ typedef struct sfa_pager sfa_pager;
 typedef struct sfa_pager_config {
     int32_t n_layer;
     int32_t n_head, n_head_kv, head_dim;
-    int32_t kv_type;       /* SFA_KV_F16 or SFA_KV_Q8_0                              */
+    int32_t kv_type;       /* SFA_KV_F32, SFA_KV_F16 or SFA_KV_Q8_0                  */
     int32_t page_size;     /* positions per page, a multiple of 32                   */
     int32_t n_seq;         /* sequences decoded together                             */
     int32_t n_ctx;         /* positions per sequence (KvStore capacity)              */
@@ -91,7 +91,7 @@ SFA_API int sfa_pager_rope_append(sfa_pager *pager, int32_t layer, float *q, con
  * f32 device, out [n_tokens][n_head * head_dim] f32 device.  A step with one
  * token per sequence runs sfa_attn_decode over the batch (split plan sized for
  * n_ctx when lossless, `window` when windowed); other steps run
- * sfa_attn_prefill per sequence (lossless F16 caches only). */
+ * sfa_attn_prefill per sequence (lossless F32 and F16 caches only). */
 SFA_API int sfa_pager_attend(sfa_pager *pager, int32_t layer, const float *q, float *out,
                              void *stream);
 

@@ -33,7 +33,8 @@ int check_desc(const sfa_kv_desc *kv) {
         return SFA_ERR_INVALID_ARGUMENT;
     if (kv->head_dim != 32 && kv->head_dim != 64 && kv->head_dim != 128) return SFA_ERR_UNSUPPORTED;
     if (kv->page_size <= 0 || kv->page_size % sfa::kTile != 0) return SFA_ERR_INVALID_ARGUMENT;
-    if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0) return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type != SFA_KV_F32 && kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0)
+        return SFA_ERR_UNSUPPORTED;
     if (kv->n_pages < 0 || kv->n_cold_pages < 0) return SFA_ERR_INVALID_ARGUMENT;
     if (kv->n_pages > 0 && (kv->k_pages == nullptr || kv->v_pages == nullptr))
         return SFA_ERR_INVALID_ARGUMENT;

@@ -29,6 +29,7 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // Row bytes of one (position, kv head) row for a cache type; 0 if unsupported.
 __host__ __device__ inline int row_bytes_of(int kv_type, int head_dim) {
     switch (kv_type) {
+    case SFA_KV_F32: return head_dim * 4;
     case SFA_KV_F16: return head_dim * 2;
     case SFA_KV_Q8_0: return (head_dim / kQK) * kQ8Bytes;
     default: return 0;

@@ -1,9 +1,10 @@
-// sfa_decode.hip - split-K paged decode attention for gfx950 (f16 KV).
+// sfa_decode.hip - split-K paged decode attention for gfx950 (f16 and Q8_0 KV).
 //
 // Replaces kq = mul_mat(k, q) -> soft_max_ext(kq, 0-mask, scale) -> mul_mat(vt, kq)
 // of build_kv_attention (src/model/engine/engine.cpp:1751-1761) for one query
-// token per sequence.  One workgroup = (sequence b, kv head, split s); its four
-// waves walk 32-position tiles of the split.  Per tile a wave
+// token per sequence.  One workgroup = one slot of a kv head's row, which the
+// split plan below maps to a (sequence, split); its four waves walk the
+// split's 32-position tiles.  Per tile a wave of the f16 kernel
 //   - loads the 32 K rows straight into the A operand of v_mfma_f32_32x32x16_f16
 //     (lane = position, 8 consecutive dims per lane, 16-byte loads),
 //   - computes S^T = K * Q^T on MFMA.  Q^T's 32 columns hold the g query heads of
@@ -564,6 +565,238 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
                           wave, n, hh);
 }
 
+// F32 decode: the reference's own cache type.  ggml's F32 path keeps Q, K,
+// P and V in f32 (the vec_dot_type of F32 is F32), so both products run on
+// v_mfma_f32_32x32x2_f32 with the f16 kernel's layouts: lane (n, hh) holds
+// half a K row (dims HD/2*hh ..) as the A operand, Q^T column n (head n % g)
+// comes from LDS, S^T lands as in the f16 kernel, and P^T step s of the PV
+// product is exactly the lane's score register s (positions 8(s/4) + 4hh +
+// s%4), so P never moves.  V tiles go straight from the page into the wave's
+// LDS region (global_load_lds, 1 KB per instruction, no registers); V^T
+// operands are 4-byte LDS reads.  Per 32-position tile a wave issues 128
+// MFMAs; at 4 bytes per element the kernel stays bound by HBM at long
+// contexts.
+template <int HD, int G>
+__global__ __launch_bounds__(256, 2) void decode_f32_kernel(DecodeParams p) {
+    static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
+    static_assert(G >= 1 && G <= 32 && (32 % G) == 0, "group size");
+    constexpr int KH = HD / 2;           // K floats per lane (half a row)
+    constexpr int KV4 = KH / 4;          // 16-byte K loads per lane
+    constexpr int DB = HD / 32;          // 32-dim blocks of the PV output
+    constexpr int VRB = HD * 4;          // V row bytes in LDS (unpadded)
+    constexpr int CPR = VRB / 16;        // 16-byte chunks per V row
+    constexpr int RPI = kWave / CPR;     // V rows per global_load_lds instruction
+    constexpr int VIT = kTile / RPI;     // V instructions per tile
+    typedef __attribute__((address_space(3))) void lds_void;
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[kDecodeWaves][kTile * VRB];
+    __shared__ float lds_m[kDecodeWaves][G];
+    __shared__ float lds_l[kDecodeWaves][G];
+    __shared__ __attribute__((aligned(16))) float lds_q[G * HD];
+    __shared__ float lds_o[kDecodeWaves][G][HD];
+
+    const int kvh = (int)blockIdx.x / p.split_row;
+    const int slot = (int)blockIdx.x - kvh * p.split_row;
+    int b_g = slot / p.guess_splits;
+    if (b_g >= p.n_seq) b_g = p.n_seq - 1;
+    const int split_g = slot - b_g * p.guess_splits;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+    const int32_t *pt = p.page_table + (int64_t)b_g * p.max_pages;
+
+    const int Hkv = p.n_head_kv;
+    const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
+    uint8_t *vt = lds_v[wave];
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+    // K of tile t into registers (row n, dims KH*hh ..), V of tile t into the
+    // wave's LDS tile (instruction i: rows i*RPI + lane/CPR, chunk lane%CPR,
+    // lane l at byte 16 l of the instruction's 1 KB run).  Both return false
+    // (wave-uniform) for an invalid page id and then load nothing.
+    floatx4 kf[KV4];
+    PageWindow pages;
+    const uint8_t *vsrc_next = nullptr;
+    auto issue_k = [&](int t) -> bool {
+        const int pos0 = t * kTile;
+        const int lpage = pos0 / p.page_size;
+        vsrc_next = nullptr;
+        if (lpage >= p.max_pages) return false;
+        const int32_t pid = pages.get(pt, p.max_pages, lpage, lane);
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        if (kb == nullptr || vb == nullptr) return false;
+        const int64_t off0 = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
+        const uint8_t *kr = kb + off0 + (int64_t)n * col_bytes + KH * 4 * hh;
+#pragma unroll
+        for (int j = 0; j < KV4; ++j) kf[j] = *reinterpret_cast<const floatx4 *>(kr + 16 * j);
+        vsrc_next = vb + off0;
+        return true;
+    };
+    // the V half of the tile issue_k last resolved (nothing for an invalid page)
+    auto issue_v = [&]() {
+        if (vsrc_next == nullptr) return;
+#pragma unroll
+        for (int i = 0; i < VIT; ++i) {
+            const int r = i * RPI + lane / CPR;
+            __builtin_amdgcn_global_load_lds(vsrc_next + (int64_t)r * col_bytes + 16 * (lane % CPR),
+                                             (lds_void *)(vt + 1024 * i), 16, 0, 0);
+        }
+    };
+
+    int t_guess, t_guess_hi;
+    split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
+    t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave);
+    pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
+    const PlanRaw raw = plan_load(p, lane);
+    // Q of the g heads in f32, staged once per workgroup in LDS
+    floatx4 qx[(G * HD / 4 + 255) / 256];
+    auto load_q = [&](int bq) {
+        const floatx4 *qr = reinterpret_cast<const floatx4 *>(p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
+#pragma unroll
+        for (int j = 0; j < (G * HD / 4 + 255) / 256; ++j) {
+            const int idx = j * 256 + (int)threadIdx.x;
+            if (idx < G * HD / 4) qx[j] = qr[idx];
+        }
+    };
+    load_q(b_g);
+    bool tile_ok = issue_k(t_guess);
+    bool v_pending = tile_ok;  // the guessed tile's V loads are in flight into vt
+    issue_v();
+
+    SlotPlan sp;
+    if (!plan(p, raw, slot, -1, lane, sp)) {
+        if (p.n_seq == 1 && slot == 0 && sp.n_b == 0) {
+            float *out0 = p.out + (int64_t)kvh * G * HD;
+            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out0[i] = 0.0f;
+        }
+        // the wave's LDS loads must land before the workgroup ends
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
+    }
+    const int b = sp.b;
+    int tile_lo, tile_hi;
+    split_tiles(sp.g.t0, sp.g.n_tiles, sp.n_b, sp.split, tile_lo, tile_hi);
+    if (b != b_g) {
+        pt = p.page_table + (int64_t)b * p.max_pages;
+        pages.load(pt, p.max_pages, tile_lo * kTile / p.page_size, lane);
+        load_q(b);
+    }
+#pragma unroll
+    for (int j = 0; j < (G * HD / 4 + 255) / 256; ++j) {
+        const int idx = j * 256 + (int)threadIdx.x;
+        if (idx < G * HD / 4) reinterpret_cast<floatx4 *>(lds_q)[idx] = qx[j];
+    }
+
+    const int lo = sp.g.lo, n_kv = sp.g.n_kv;
+    float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
+    int t = tile_lo + wave_u;
+    if (t != t_guess || b != b_g) {
+        // the guessed V loads write vt: let them land before the real ones
+        if (v_pending) __builtin_amdgcn_s_waitcnt(0);
+        if (t < tile_hi) {
+            tile_ok = issue_k(t);
+        } else {
+            tile_ok = false;
+            vsrc_next = nullptr;
+        }
+        issue_v();
+    }
+    __syncthreads();
+    const float *qcol = lds_q + (n % G) * HD + KH * hh;
+    // V^T operand of step s, dim block d: row 8(s/4) + 4hh + s%4, dim 32d + n
+    const uint8_t *vrow = vt + (4 * hh) * VRB + 4 * n;
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+
+    bool first = true;
+    for (; t < tile_hi; t += kDecodeWaves) {
+        const int pos0 = t * kTile;
+        const bool dead = !tile_ok;
+        // S^T = K * Q^T, two accumulation chains
+        floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+        for (int j = 0; j < KV4; ++j) {
+            const floatx4 qv = *reinterpret_cast<const floatx4 *>(qcol + 4 * j);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][0], qv[0], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][1], qv[1], s1, 0, 0, 0);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][2], qv[2], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][3], qv[3], s1, 0, 0, 0);
+        }
+        s0 += s1;
+        // registers are free: fetch the next tile's K (its V follows the P*V)
+        const bool next_ok = t + kDecodeWaves < tile_hi ? issue_k(t + kDecodeWaves) : false;
+
+        const bool interior = !dead && pos0 >= lo && pos0 + kTile <= n_kv;
+        float sv[16];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float v = s0[i] * p.scale_log2;
+            if (!interior) {
+                const int pp = pos0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                v = (!dead && pp >= lo && pp < n_kv) ? v : -INFINITY;
+            }
+            sv[i] = v;
+            mt = fmaxf(mt, v);
+        }
+        if (__any(mt > m_run + kRescaleLog2)) {
+            mt = fmaxf(mt, xor32(mt));
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+            if (!first) {
+#pragma unroll
+                for (int d = 0; d < DB; ++d) o[d] *= alpha;
+            }
+            m_run = m_new;
+        }
+        first = false;
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        float pe[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pe[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
+            l_run += pe[i];
+        }
+
+        // this tile's V has landed in vt (the next tile's K loads, issued after
+        // it, may still fly: loads complete in order); then O^T += V^T * P^T,
+        // rows outside [lo, n_kv) read as 0
+        // (a page's unused tail may hold any bytes)
+        if (next_ok)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KV4) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int sidx = 0; sidx < 16; ++sidx) {
+            const int r = 8 * (sidx >> 2) + (sidx & 3);  // + 4hh through vrow
+            const bool row_ok = interior || (!dead && pos0 + r + 4 * hh >= lo && pos0 + r + 4 * hh < n_kv);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                float va = *reinterpret_cast<const float *>(vrow + r * VRB + 128 * d);
+                va = row_ok ? va : 0.0f;
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(va, pe[sidx], o[d], 0, 0, 0);
+            }
+        }
+        // every V^T read of this tile has returned before the next tile's V
+        // overwrites vt
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (next_ok) issue_v();
+        tile_ok = next_ok;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+
+    l_run += xor32(l_run);
+    split_epilogue<HD, G>(o, m_run, l_run, lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b,
+                          wave, n, hh);
+}
+
 // Q8_0 decode (head_dim 64 or 128).  A row is head_dim/32 ggml block_q8_0
 // records {fp16 d; int8 q[32]} of 34 bytes; rows start 4-byte aligned (the
 // row is 68 or 136 bytes), so block c starts at 2c mod 4 and every byte
@@ -1088,6 +1321,8 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
         if (p.kv_type == SFA_KV_Q8_0) {
             if constexpr (HD >= 64 && G <= 8)
                 hipLaunchKernelGGL((decode_q8_kernel<HD, G>), grid, dim3(256), 0, s, p);
+        } else if (p.kv_type == SFA_KV_F32) {
+            hipLaunchKernelGGL((decode_f32_kernel<HD, G>), grid, dim3(256), 0, s, p);
         } else {
             hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
         }
@@ -1151,7 +1386,8 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     p.part = static_cast<float *>(workspace);
 
     p.kv_type = kv->kv_type;
-    if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0) return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type != SFA_KV_F32 && kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0)
+        return SFA_ERR_UNSUPPORTED;
     if (kv->kv_type == SFA_KV_Q8_0 && HD < 64) return SFA_ERR_UNSUPPORTED;
     int rc;
     switch (HD) {

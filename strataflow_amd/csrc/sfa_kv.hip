@@ -2,7 +2,8 @@
 //
 // The append is the ggml_cpy of Kcur/Vcur into the cache column of each token
 // (src/model/engine/engine.cpp:1646-1656), with the conversion a cpy into the
-// cache type performs: F16 rounds to nearest even; Q8_0 quantises each 32-block
+// cache type performs: F32 copies (the reference's own cache type); F16 rounds
+// to nearest even; Q8_0 quantises each 32-block
 // with d = amax/127 (stored fp16) and q = round(x * (1/d)).  Division and
 // reciprocal are IEEE-correct here (no fast-math), so the bytes written equal a
 // CPU quantiser's bit for bit.
@@ -57,6 +58,12 @@ __device__ inline void store_f16x8(uint8_t *dst, const float (&x)[8]) {
     *reinterpret_cast<half8 *>(dst) = h;
 }
 
+// 8 consecutive elements of a row stored as f32, two 16-byte stores.
+__device__ inline void store_f32x8(uint8_t *dst, const float (&x)[8]) {
+    reinterpret_cast<floatx4 *>(dst)[0] = floatx4{x[0], x[1], x[2], x[3]};
+    reinterpret_cast<floatx4 *>(dst)[1] = floatx4{x[4], x[5], x[6], x[7]};
+}
+
 // One 32-element block -> block_q8_0 (quantize_row_q8_0 semantics): d =
 // amax / 127 stored fp16, q = round(x * (1/d)).  The block starts 2-byte
 // aligned: d and the quants are stored as 16-bit words.
@@ -88,8 +95,9 @@ __device__ inline void load_f32(const float *src, float (&x)[N]) {
     }
 }
 
-// One thread per 8 elements of a row: f32 -> f16 (RNE), 16-byte store.
-__global__ __launch_bounds__(256) void append_f16_kernel(AppendParams p) {
+// One thread per 8 elements of a row: f32 -> f16 (RNE) or f32 as is.
+template <int KVT>
+__global__ __launch_bounds__(256) void append_e8_kernel(AppendParams p) {
     const int chunks = p.head_dim / 8;
     const int64_t total = (int64_t)p.n_tok * p.n_head_kv * chunks * 2;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -104,7 +112,10 @@ __global__ __launch_bounds__(256) void append_f16_kernel(AppendParams p) {
     if (dst == nullptr) return;
     float x[8];
     load_f32<8>((which ? p.v : p.k) + ((int64_t)tok * p.n_head_kv + kvh) * p.head_dim + 8 * c, x);
-    store_f16x8(dst + 16 * c, x);
+    if constexpr (KVT == SFA_KV_F16)
+        store_f16x8(dst + 16 * c, x);
+    else
+        store_f32x8(dst + 32 * c, x);
 }
 
 // One thread per 32-element block: quantize_row_q8_0 semantics.
@@ -142,7 +153,7 @@ constexpr int kRopeQPairs = 8;  // Q pairs per thread loaded ahead (32 heads x 6
 template <int KVT>
 __global__ __launch_bounds__(256) void rope_append_kernel(AppendParams p, float *q, int n_head,
                                                           float theta_scale) {
-    constexpr int E = KVT == SFA_KV_F16 ? 8 : kQK;  // elements per K/V unit of work
+    constexpr int E = KVT == SFA_KV_Q8_0 ? kQK : 8;  // elements per K/V unit of work
     __shared__ float cs[kMaxHalfDim][2];
     const int tok = blockIdx.x;
     const int ps = p.pos[tok];
@@ -212,6 +223,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(AppendParams p, float 
         }
         if constexpr (KVT == SFA_KV_F16)
             store_f16x8(dst + 16 * un, xs);
+        else if constexpr (KVT == SFA_KV_F32)
+            store_f32x8(dst + 32 * un, xs);
         else
             store_q8_block(dst + kQ8Bytes * un, xs);
     };
@@ -265,10 +278,13 @@ int append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const i
         return SFA_ERR_INVALID_ARGUMENT;
     AppendParams p = append_params(kv, k, v, seq, pos, n_tok, page_table, max_pages);
     int64_t total;
-    if (kv->kv_type == SFA_KV_F16) {
+    if (kv->kv_type == SFA_KV_F16 || kv->kv_type == SFA_KV_F32) {
         total = (int64_t)n_tok * kv->n_head_kv * (kv->head_dim / 8) * 2;
-        hipLaunchKernelGGL(append_f16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                           stream, p);
+        const dim3 grid((unsigned)((total + 255) / 256));
+        if (kv->kv_type == SFA_KV_F16)
+            hipLaunchKernelGGL(append_e8_kernel<SFA_KV_F16>, grid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL(append_e8_kernel<SFA_KV_F32>, grid, dim3(256), 0, stream, p);
     } else if (kv->kv_type == SFA_KV_Q8_0) {
         total = (int64_t)n_tok * kv->n_head_kv * (kv->head_dim / kQK) * 2;
         hipLaunchKernelGGL(append_q8_0_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
@@ -302,6 +318,9 @@ int rope_append_launch(const sfa_kv_desc *kv, float *q, const float *k, const fl
     const float theta_scale = powf(freq_base, -2.0f / (float)kv->head_dim);
     if (kv->kv_type == SFA_KV_F16) {
         hipLaunchKernelGGL(rope_append_kernel<SFA_KV_F16>, dim3((unsigned)n_tok), dim3(256), 0, stream, p, q,
+                           kv->n_head, theta_scale);
+    } else if (kv->kv_type == SFA_KV_F32) {
+        hipLaunchKernelGGL(rope_append_kernel<SFA_KV_F32>, dim3((unsigned)n_tok), dim3(256), 0, stream, p, q,
                            kv->n_head, theta_scale);
     } else if (kv->kv_type == SFA_KV_Q8_0) {
         hipLaunchKernelGGL(rope_append_kernel<SFA_KV_Q8_0>, dim3((unsigned)n_tok), dim3(256), 0, stream, p, q,

@@ -303,18 +303,215 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     }
 }
 
+// F32 cache (the reference's own type): ggml converts nothing, so both
+// products run on v_mfma_f32_32x32x2_f32 with Q, K, P and V in f32, in the
+// layouts of prefill_f16_kernel (S^T with the lane owning its query row, P^T
+// step s of a 32-position block = the lane's score register s).  K and V
+// tiles go from the page straight into LDS (global_load_lds, 1 KB per
+// instruction): K chunks are XOR-swizzled by row so the 16 rows one ds_read_b128
+// phase touches cover all 64 banks; V chunks of rows with bit 2 set are
+// shifted by 128 bytes so the two lane halves of a V^T read (rows 4 apart)
+// use disjoint banks.  Rows outside the attended range (and tiles of an
+// invalid page) are masked in the scores and read as 0 for P*V.
 template <int HD, int G>
-static void launch_prefill(const PrefillParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((prefill_f16_kernel<HD, G>), dim3(p.n_qblk * p.n_head_kv), dim3(256), 0, s, p);
+__global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
+    constexpr int KH = HD / 2;           // Q / K floats per lane (half a row)
+    constexpr int DB = HD / 32;
+    constexpr int QB = 128 / G;
+    constexpr int RB = HD * 4;           // row bytes
+    constexpr int CPR = RB / 16;         // 16-byte chunks per row
+    constexpr int TB = kPBN * RB;        // tile bytes (K or V)
+    constexpr int IPW = TB / 1024 / 4;   // 1 KB load instructions per wave per tile (K or V)
+    constexpr int KSW = (CPR < 16 ? CPR : 16) - 1;  // K chunk swizzle mask (row bits)
+    constexpr int VSW = CPR >= 16 ? 8 : CPR / 2;    // V chunk shift for rows with bit 2 set
+    static_assert(TB % 4096 == 0, "tile split over four waves");
+    typedef __attribute__((address_space(3))) void lds_void;
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][TB];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][TB];
+
+    const int kvh = (int)blockIdx.x % p.n_head_kv;
+    const int qblk = p.n_qblk - 1 - (int)blockIdx.x / p.n_head_kv;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+    const int64_t col_bytes = (int64_t)p.n_head_kv * RB;
+
+    const int rho = wave * 32 + n;
+    const int g = rho / QB;
+    const int tq = qblk * QB + rho % QB;
+    const bool row_ok = tq < p.T;
+    const int h = kvh * G + g;
+    const int qp = p.q_pos0 + tq;
+
+    const int first_tok = qblk * QB;
+    int last_tok = first_tok + QB - 1;
+    if (last_tok > p.T - 1) last_tok = p.T - 1;
+    const int kv_hi = p.q_pos0 + last_tok;
+    const int q_lo = p.q_pos0 + first_tok;
+    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
+    const int tile0 = lo / kPBN;
+    const int tile1 = kv_hi / kPBN;
+    const bool block_full = (qblk + 1) * QB <= p.T;
+
+    // tile t -> LDS buffer buf; false (workgroup-uniform) for an invalid page
+    auto load = [&](int t, int buf) -> bool {
+        const int pos0 = t * kPBN;
+        const int lp = pos0 / p.page_size;
+        const int32_t pid = __builtin_amdgcn_readfirstlane(lp < p.max_pages ? p.page_table[lp] : -1);
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        if (kb == nullptr || vb == nullptr) return false;
+        const int64_t base = (int64_t)(pos0 - lp * p.page_size) * col_bytes + (int64_t)kvh * RB;
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+            const int blk = wave * IPW + i;      // 1 KB block of the tile
+            const int cid = blk * 64 + lane;     // LDS chunk this lane fills
+            const int r = cid / CPR, cp = cid % CPR;
+            const int ck = cp ^ (r & KSW);
+            const int cv = cp ^ (((r >> 2) & 1) * VSW);
+            __builtin_amdgcn_global_load_lds(kb + base + (int64_t)r * col_bytes + 16 * ck,
+                                             (lds_void *)(&lds_k[buf][1024 * blk]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vb + base + (int64_t)r * col_bytes + 16 * cv,
+                                             (lds_void *)(&lds_v[buf][1024 * blk]), 16, 0, 0);
+        }
+        return true;
+    };
+
+    bool ok_cur = load(tile0, 0);
+    // Q of this lane's row, dims KH*hh .. KH*hh + KH - 1 (rows past T read row 0, zeroed)
+    float qf[KH];
+    {
+        const floatx4 *qr = reinterpret_cast<const floatx4 *>(
+            p.q + ((int64_t)(row_ok ? tq : 0) * p.n_head + h) * HD + KH * hh);
+#pragma unroll
+        for (int j = 0; j < KH / 4; ++j) {
+            const floatx4 v4 = qr[j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qf[4 * j + e] = row_ok ? v4[e] : 0.0f;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    for (int t = tile0; t <= tile1; ++t) {
+        const int buf = (t - tile0) & 1;
+        const int pos0 = t * kPBN;
+        const bool ok_next = t < tile1 ? load(t + 1, buf ^ 1) : false;  // in flight meanwhile
+        const uint8_t *kt = lds_k[buf];
+        const uint8_t *vt = lds_v[buf];
+        const bool dead = !ok_cur;
+
+        floatx16 s[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+            const int r = 32 * pb + n;
+#pragma unroll
+            for (int j = 0; j < KH / 4; ++j) {
+                const int ch = (KH * hh) / 4 + j;
+                const floatx4 a = *reinterpret_cast<const floatx4 *>(kt + r * RB + 16 * (ch ^ (r & KSW)));
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    s[pb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qf[4 * j + e], s[pb], 0, 0, 0);
+            }
+        }
+        const bool edge = dead || pos0 < lo || pos0 + kPBN - 1 > q_lo || !block_full;
+        if (edge) {
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
+                    s[pb][i] = (!dead && row_ok && kp >= lo && kp <= qp) ? s[pb][i] : -INFINITY;
+                }
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
+        mt = fmaxf(mt, xor32(mt)) * p.scale_log2;
+        float alpha = 1.0f;
+        if (mt > m_run + kRescaleLog2) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mt);
+            m_run = mt;
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        float pe[2][16];
+        float ls = 0.0f;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                pe[pb][i] = __builtin_amdgcn_exp2f(fmaf(s[pb][i], p.scale_log2, -m_use));
+                ls += pe[pb][i];
+            }
+        }
+        l_run = l_run * alpha + ls;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d) o[d] *= alpha;
+        }
+        // O^T += V^T * P^T: step s of block pb reads row 32pb + 8(s/4) + 4hh + s%4
+        // (its chunk shifted by hh * VSW), dim 32d + n
+        const uint8_t *vl = vt + (4 * hh) * RB + 4 * (n & 3);
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+            for (int sidx = 0; sidx < 16; ++sidx) {
+                const int r = 32 * pb + 8 * (sidx >> 2) + (sidx & 3);  // + 4hh through vl
+                const bool vok = !edge || (!dead && pos0 + r + 4 * hh >= lo && pos0 + r + 4 * hh <= kv_hi);
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+                    const int ch = (32 * d + n) / 4;
+                    float va = *reinterpret_cast<const float *>(vl + r * RB + 16 * (ch ^ (hh * VSW)));
+                    va = vok ? va : 0.0f;
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(va, pe[pb][sidx], o[d], 0, 0, 0);
+                }
+            }
+        }
+        // the next tile's loads have landed in every wave before anyone reads them
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        ok_cur = ok_next;
+    }
+
+    l_run += xor32(l_run);
+    if (row_ok) {
+        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+        float *orow = p.out + ((int64_t)tq * p.n_head + h) * HD;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                orow[32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i] * inv;
+            }
+        }
+    }
+}
+
+template <int HD, int G>
+static void launch_prefill(const PrefillParams &p, int kv_type, hipStream_t s) {
+    if (kv_type == SFA_KV_F32)
+        hipLaunchKernelGGL((prefill_f32_kernel<HD, G>), dim3(p.n_qblk * p.n_head_kv), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((prefill_f16_kernel<HD, G>), dim3(p.n_qblk * p.n_head_kv), dim3(256), 0, s, p);
 }
 
 template <int HD>
-static int launch_prefill_g(const PrefillParams &p, int G, hipStream_t s) {
+static int launch_prefill_g(const PrefillParams &p, int G, int kv_type, hipStream_t s) {
     switch (G) {
-    case 1: launch_prefill<HD, 1>(p, s); return SFA_OK;
-    case 2: launch_prefill<HD, 2>(p, s); return SFA_OK;
-    case 4: launch_prefill<HD, 4>(p, s); return SFA_OK;
-    case 8: launch_prefill<HD, 8>(p, s); return SFA_OK;
+    case 1: launch_prefill<HD, 1>(p, kv_type, s); return SFA_OK;
+    case 2: launch_prefill<HD, 2>(p, kv_type, s); return SFA_OK;
+    case 4: launch_prefill<HD, 4>(p, kv_type, s); return SFA_OK;
+    case 8: launch_prefill<HD, 8>(p, kv_type, s); return SFA_OK;
     default: return SFA_ERR_UNSUPPORTED;
     }
 }
@@ -322,7 +519,7 @@ static int launch_prefill_g(const PrefillParams &p, int G, hipStream_t s) {
 int prefill_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
                    int32_t max_pages, int32_t q_pos0, int32_t T, int32_t kv_lo, float scale,
                    hipStream_t stream) {
-    if (kv->kv_type != SFA_KV_F16) return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_F32) return SFA_ERR_UNSUPPORTED;
     if (kv->page_size % kPBN != 0) return SFA_ERR_UNSUPPORTED;
     if (q == nullptr || out == nullptr || page_table == nullptr) return SFA_ERR_INVALID_ARGUMENT;
     if (T < 0 || q_pos0 < 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
@@ -334,7 +531,7 @@ int prefill_launch(const sfa_kv_desc *kv, const float *q, float *out, const int3
     p.v_pages = static_cast<const uint8_t *>(kv->v_pages);
     p.k_cold = static_cast<const uint8_t *>(kv->k_cold);
     p.v_cold = static_cast<const uint8_t *>(kv->v_cold);
-    p.page_bytes = (int64_t)kv->head_dim * 2 * kv->n_head_kv * kv->page_size;
+    p.page_bytes = (int64_t)row_bytes_of(kv->kv_type, kv->head_dim) * kv->n_head_kv * kv->page_size;
     p.n_pages = kv->n_pages;
     p.n_cold = kv->n_cold_pages;
     p.page_size = kv->page_size;
@@ -352,9 +549,9 @@ int prefill_launch(const sfa_kv_desc *kv, const float *q, float *out, const int3
     p.scale_log2 = scale * 1.4426950408889634f;
     int rc;
     switch (kv->head_dim) {
-    case 32: rc = launch_prefill_g<32>(p, G, stream); break;
-    case 64: rc = launch_prefill_g<64>(p, G, stream); break;
-    case 128: rc = launch_prefill_g<128>(p, G, stream); break;
+    case 32: rc = launch_prefill_g<32>(p, G, kv->kv_type, stream); break;
+    case 64: rc = launch_prefill_g<64>(p, G, kv->kv_type, stream); break;
+    case 128: rc = launch_prefill_g<128>(p, G, kv->kv_type, stream); break;
     default: return SFA_ERR_UNSUPPORTED;
     }
     if (rc != SFA_OK) return rc;

@@ -15,12 +15,14 @@ import math
 import torch
 
 from . import _lib
-from ._lib import SFA_KV_F16, SFA_KV_Q8_0, SfaKvDesc
+from ._lib import SFA_KV_F16, SFA_KV_F32, SFA_KV_Q8_0, SfaKvDesc
 
-__all__ = ["PagedKV", "row_bytes", "SFA_KV_F16", "SFA_KV_Q8_0"]
+__all__ = ["PagedKV", "row_bytes", "SFA_KV_F32", "SFA_KV_F16", "SFA_KV_Q8_0"]
 
 
 def row_bytes(kv_type: int, head_dim: int) -> int:
+    if kv_type == SFA_KV_F32:
+        return head_dim * 4
     if kv_type == SFA_KV_F16:
         return head_dim * 2
     if kv_type == SFA_KV_Q8_0:

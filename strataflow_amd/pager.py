@@ -14,9 +14,10 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, SFA_KV_Q8_0
+from ._lib import SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, SFA_KV_F32, SFA_KV_Q8_0
 
-__all__ = ["KvPager", "SFA_ATTEND_LOSSLESS", "SFA_ATTEND_WINDOW", "SFA_KV_F16", "SFA_KV_Q8_0"]
+__all__ = ["KvPager", "SFA_ATTEND_LOSSLESS", "SFA_ATTEND_WINDOW", "SFA_KV_F32", "SFA_KV_F16",
+           "SFA_KV_Q8_0"]
 
 
 def _stream() -> int:

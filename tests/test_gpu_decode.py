@@ -251,3 +251,61 @@ def test_decode_one_sequence_beyond_max_seq_len(gpu, oracle_mod):
     c = Case(oracle_mod, seq_lens=[1500], seed=211)
     out = c.decode(max_seq_len=100)
     assert_close(out, c.oracle(oracle_mod.GGML), what="one sequence beyond max_seq_len")
+
+
+# ---- F32 KV (the reference's own cache type) -----------------------------------
+# ggml converts nothing for an F32 cache, so the kernel (f32 MFMA for both
+# products, P kept in f32) tracks the ggml-semantics oracle to f32 accumulation
+# rounding; the bars are 50x tighter than the parity bar, so an f16 rounding of
+# Q, K, P or V anywhere would fail them.
+F32_MAX_ABS, F32_REL = 4e-5, 2e-5
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128), (8, 4, 32), (8, 8, 64), (16, 2, 128)])
+@pytest.mark.parametrize("n_kv", [1, 33, 257, 1000])
+def test_decode_f32_shapes(gpu, oracle_mod, shape, n_kv):
+    Hq, Hkv, hd = shape
+    c = Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, page_size=64,
+             kv_type=0, seed=n_kv + hd + 3)
+    out = c.decode()
+    assert_close(out, c.oracle(oracle_mod.GGML), max_abs=F32_MAX_ABS, rel_l2=F32_REL,
+                 what=f"f32 {shape} n_kv={n_kv} vs ggml")
+
+
+def test_decode_f32_ctx4096_and_placement(gpu, oracle_mod):
+    import torch
+    c = Case(oracle_mod, seq_lens=[4096], kv_type=0, seed=48, extra_pages=2)
+    base = c.decode()
+    ma, rl = assert_close(base, c.oracle(oracle_mod.GGML), max_abs=F32_MAX_ABS, rel_l2=F32_REL,
+                          what="f32 ctx4096 vs ggml")
+    print(f"f32 ctx4096: max_abs {ma:.2e} rel_l2 {rl:.2e}")
+    perm = np.random.default_rng(4).permutation(c.n_pages).astype(np.int32)
+    k2 = torch.empty_like(c.dev.k[0]); v2 = torch.empty_like(c.dev.v[0])
+    idx = torch.from_numpy(perm).long().to(gpu)
+    k2[idx] = c.dev.k[0]; v2[idx] = c.dev.v[0]
+    c.dev.k[0].copy_(k2); c.dev.v[0].copy_(v2)
+    pt = c.page_table.copy(); valid = pt >= 0; pt[valid] = perm[pt[valid]]
+    c.t_pt = torch.from_numpy(pt).to(gpu)
+    assert np.array_equal(c.decode().view(np.uint32), base.view(np.uint32))
+
+
+@pytest.mark.parametrize("page_size", [32, 512])
+def test_decode_f32_varlen_window(gpu, oracle_mod, page_size):
+    seq = [0, 1, 2500, 777, 64, 300]
+    lo = [0, 0, 1999, 13, 32, 290]
+    c = Case(oracle_mod, seq_lens=seq, kv_lo=lo, kv_type=0, page_size=page_size, seed=page_size + 5)
+    out = c.decode(max_seq_len=2500)
+    assert_close(out, c.oracle(oracle_mod.GGML), max_abs=F32_MAX_ABS, rel_l2=F32_REL,
+                 what=f"f32 varlen page {page_size}")
+    assert np.all(out[0] == 0)
+
+
+@pytest.mark.parametrize("B", [3, 70])
+def test_decode_f32_batches(gpu, oracle_mod, B):
+    rng = np.random.default_rng(300 + B)
+    seq = rng.integers(0, 1500, B)
+    seq[0] = 0
+    c = Case(oracle_mod, seq_lens=seq, n_head=8, n_head_kv=2, head_dim=128, kv_type=0, seed=310 + B)
+    out = c.decode(max_seq_len=1600)
+    assert_close(out, c.oracle(oracle_mod.GGML), max_abs=F32_MAX_ABS, rel_l2=F32_REL,
+                 what=f"f32 B={B}")

@@ -1,5 +1,6 @@
 """KV append on the GPU (sfa_kv_append) writes the same bytes as the oracle's
-ggml_cpy restatement: f16 round-to-nearest-even and Q8_0 quantisation."""
+ggml_cpy restatement: f32 as is, f16 round-to-nearest-even and Q8_0
+quantisation."""
 from __future__ import annotations
 
 import numpy as np
@@ -8,7 +9,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("kv_type", [1, 8])
+@pytest.mark.parametrize("kv_type", [0, 1, 8])
 @pytest.mark.parametrize("hd", [32, 128])
 def test_append_bit_exact(gpu, oracle_mod, kv_type, hd):
     import torch

@@ -14,8 +14,8 @@ import pytest
 import torch
 
 from strataflow_amd import synth
-from strataflow_amd.pager import (SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, SFA_KV_Q8_0,
-                                  KvPager)
+from strataflow_amd.pager import (SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, SFA_KV_F32,
+                                  SFA_KV_Q8_0, KvPager)
 from strataflow_amd.paged_kv import PagedKV
 
 from .helpers import assert_close
@@ -106,7 +106,7 @@ def _decode_and_compare(m, n_steps, check_every=1):
     return outs
 
 
-@pytest.mark.parametrize("kv_type", [SFA_KV_F16, SFA_KV_Q8_0])
+@pytest.mark.parametrize("kv_type", [SFA_KV_F32, SFA_KV_F16, SFA_KV_Q8_0])
 def test_pager_lossless_bit_identical(gpu, oracle_mod, kv_type):
     # 4 sequences of different lengths, window of 4 pages, ragged first fill
     host = oracle_mod.HostPagedKv(8, 128, 256, kv_type, 4 * 32 + 2)
@@ -121,7 +121,8 @@ def test_pager_lossless_bit_identical(gpu, oracle_mod, kv_type):
     assert st["pages_evicted"] == evicted_pages > 0
     assert st["cold_pages_in_use"] == evicted_pages
     assert st["pages_dropped"] == 0
-    assert st["bytes_evicted"] == evicted_pages * 2 * 2 * 256 * 8 * (256 if kv_type == SFA_KV_F16 else 136)
+    row = {SFA_KV_F32: 512, SFA_KV_F16: 256, SFA_KV_Q8_0: 136}[kv_type]
+    assert st["bytes_evicted"] == evicted_pages * 2 * 2 * 256 * 8 * row
     assert st["dev_pages_in_use"] <= 4 * 5
     pt, used = m.pager.tables()
     assert (used == lens).all() and (pt <= -2).sum() == evicted_pages
@@ -149,10 +150,12 @@ def test_pager_window_matches_oracle(gpu, oracle_mod):
     assert_close(out.cpu().numpy(), ref, what="window paged vs oracle")
 
 
-def test_pager_prefill_chunk_over_cold_pages(gpu, oracle_mod):
+@pytest.mark.parametrize("kv_type", [SFA_KV_F32, SFA_KV_F16])
+def test_pager_prefill_chunk_over_cold_pages(gpu, oracle_mod, kv_type):
     # a 200-token chunk whose history is partly in the cold pool
-    host = oracle_mod.HostPagedKv(8, 128, 256, SFA_KV_F16, 2 * 16 + 2)
-    m = Mirror(n_seq=2, n_ctx=4096, window=512, attend=SFA_ATTEND_LOSSLESS, seed=3, oracle=host)
+    host = oracle_mod.HostPagedKv(8, 128, 256, kv_type, 2 * 16 + 2)
+    m = Mirror(n_seq=2, n_ctx=4096, window=512, attend=SFA_ATTEND_LOSSLESS, seed=3, oracle=host,
+               kv_type=kv_type)
     m.fill([1800, 700])
     pos0 = m.used.copy()
     outs = m.step(np.array([200, 0], np.int32))

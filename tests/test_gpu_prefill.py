@@ -10,7 +10,7 @@ from tests.helpers import assert_close, f16_cols, golden, scatter_columns
 pytestmark = pytest.mark.gpu
 
 
-def build(oracle_mod, gpu, *, Hq, Hkv, hd, n_cached, T, page_size=256, seed=0, bf16=False):
+def build(oracle_mod, gpu, *, Hq, Hkv, hd, n_cached, T, page_size=256, seed=0, bf16=False, kv_type=1):
     import torch
     from strataflow_amd import synth
     from strataflow_amd.paged_kv import PagedKV
@@ -18,12 +18,12 @@ def build(oracle_mod, gpu, *, Hq, Hkv, hd, n_cached, T, page_size=256, seed=0, b
     n_kv = n_cached + T
     n_pages = (n_kv + page_size - 1) // page_size + 2
     pt = synth.page_tables(rng, [n_kv], page_size, n_pages)
-    host = oracle_mod.HostPagedKv(Hkv, hd, page_size, 1, n_pages)
+    host = oracle_mod.HostPagedKv(Hkv, hd, page_size, kv_type, n_pages)
     pos = np.arange(n_kv, dtype=np.int32)
     q, k, v = synth.qkv(rng, n_kv, Hq, Hkv, hd, pos, 1e6, bf16=bf16)
     assert host.append(k, v, np.zeros(n_kv, np.int32), pos, pt) == 0
     q = np.ascontiguousarray(q[n_cached:])
-    dev = PagedKV(1, Hq, Hkv, hd, 1, page_size, n_pages, device=gpu)
+    dev = PagedKV(1, Hq, Hkv, hd, kv_type, page_size, n_pages, device=gpu)
     dev.k[0].copy_(torch.from_numpy(host.k))
     dev.v[0].copy_(torch.from_numpy(host.v))
     return host, dev, pt, q, n_kv
@@ -126,3 +126,40 @@ def test_prefill_rejects_unsupported(gpu, oracle_mod):
     # T == 0 is a no-op
     assert lib.sfa_attn_prefill(ctypes.byref(d), tq.data_ptr(), out.data_ptr(), tpt.data_ptr(),
                                 int(pt.shape[1]), 10, 0, 0, 0.17, s) == _lib.SFA_OK
+
+
+# ---- F32 cache: f32 MFMA, no operand conversion; bars 50x tighter than parity
+F32_MAX_ABS, F32_REL = 4e-5, 2e-5
+
+
+@pytest.mark.parametrize("shape,n_cached,T,kv_lo,page_size", [
+    ((32, 8, 128), 300, 256, 0, 256),
+    ((8, 4, 32), 50, 100, 0, 64),
+    ((8, 8, 64), 70, 130, 0, 128),
+    ((16, 8, 64), 333, 97, 77, 128),     # unaligned window start
+    ((32, 4, 128), 129, 260, 0, 512),    # g = 8
+    ((4, 4, 32), 0, 1, 0, 64),           # one token, no history
+])
+def test_prefill_f32_vs_oracle(gpu, oracle_mod, shape, n_cached, T, kv_lo, page_size):
+    Hq, Hkv, hd = shape
+    host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=Hq, Hkv=Hkv, hd=hd, n_cached=n_cached, T=T,
+                                   page_size=page_size, seed=T + hd + 1, kv_type=0)
+    out = run(dev, gpu, pt, q, n_cached, kv_lo)
+    ref = host.attention(q[None], Hq, pt, np.array([n_kv], np.int32), np.array([kv_lo], np.int32),
+                         T=T, mode=oracle_mod.GGML)[0].reshape(T, -1)
+    assert_close(out, ref, max_abs=F32_MAX_ABS, rel_l2=F32_REL, what=f"f32 {shape} T={T} vs ggml")
+
+
+def test_prefill_f32_rows_equal_f32_decode(gpu, oracle_mod):
+    # a causal prefill row is the decode of its position (both f32 paths)
+    import torch
+    Hq, Hkv, hd, n_cached, T = 32, 8, 128, 512, 192
+    host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=Hq, Hkv=Hkv, hd=hd, n_cached=n_cached, T=T,
+                                   seed=17, kv_type=0)
+    out = run(dev, gpu, pt, q, n_cached)
+    rows = [0, 1, 63, 64, 100, T - 1]
+    tq = torch.from_numpy(q[rows]).to(gpu)
+    tpt = torch.from_numpy(np.repeat(pt, len(rows), axis=0)).to(gpu)
+    sl = torch.tensor([n_cached + t + 1 for t in rows], dtype=torch.int32, device=gpu)
+    dec = dev.decode(0, tq, tpt, sl, n_kv).cpu().numpy().reshape(len(rows), -1)
+    assert_close(out[rows], dec, max_abs=F32_MAX_ABS, rel_l2=F32_REL, what="f32 prefill rows vs decode")

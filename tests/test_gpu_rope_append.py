@@ -4,9 +4,10 @@ against the oracle: orc_rope_normal on Q and K followed by orc_kv_append.
 Bars: rotated Q within 1e-6 of each pair's magnitude (cosf/sinf may differ by
 an ulp between the device and the host libm; theta itself follows the same f32
 recurrence on both, from the same host powf); V bytes identical (the append's
-conversion, unchanged); rotated K in an f16 cache within one f16 ulp of the
-oracle's bytes; in a Q8_0 cache the block scales within one f16 ulp and every
-dequantised value within one quantisation step."""
+conversion, unchanged); rotated K in an f32 cache within the Q bar, in an f16
+cache within one f16 ulp of the oracle's bytes; in a Q8_0 cache the block
+scales within one f16 ulp and every dequantised value within one quantisation
+step."""
 from __future__ import annotations
 
 import numpy as np
@@ -14,7 +15,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-F16, Q8 = 1, 8
+F32, F16, Q8 = 0, 1, 8
 
 
 def _tokens(rng, n_seq, per_seq, page_size, max_pages):
@@ -49,7 +50,7 @@ def _f16_ulps(a_bits, b_bits):
     return np.abs(a - b)
 
 
-@pytest.mark.parametrize("kv_type", [F16, Q8])
+@pytest.mark.parametrize("kv_type", [F32, F16, Q8])
 @pytest.mark.parametrize("shape", [(32, 8, 128), (8, 4, 32), (16, 8, 64)])
 def test_rope_append_vs_oracle(gpu, oracle_mod, kv_type, shape):
     import torch
@@ -88,7 +89,12 @@ def test_rope_append_vs_oracle(gpu, oracle_mod, kv_type, shape):
     kd = dev.k[0].cpu().numpy().reshape(n_pages, -1)
     vd = dev.v[0].cpu().numpy().reshape(n_pages, -1)
     assert np.array_equal(vd, host.v[:n_pages]), "V bytes differ from the oracle's append"
-    if kv_type == F16:
+    if kv_type == F32:
+        # the rotated K stored as is: the rotation bar of the Q check
+        rows = _rows(kd, pt, seq, pos, ps, Hkv * hd * 4).view(np.float32).reshape(n, Hkv, hd)
+        kmag = np.repeat(np.abs(k[..., 0::2]) + np.abs(k[..., 1::2]), 2, axis=-1).astype(np.float64)
+        assert np.all(np.abs(rows - k_ref) <= 1e-6 * kmag + 1e-7), float(np.max(np.abs(rows - k_ref)))
+    elif kv_type == F16:
         # per token: the device's f16 K row against the unrounded f32 oracle
         # rotation; f16 rounding (half an ulp, or 2^-25 below the normal
         # range) plus the rotation bar

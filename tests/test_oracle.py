@@ -131,7 +131,7 @@ def test_attention_matches_golden(oracle_mod, name):
     assert_close(gg, g["ggml"], max_abs=5e-5, rel_l2=2e-5, what="ggml")
 
 
-@pytest.mark.parametrize("kv_type", [1, 8])
+@pytest.mark.parametrize("kv_type", [0, 1, 8])
 def test_single_position_returns_v(oracle_mod, kv_type):
     # n_kv == 1 => p == 1 exactly => O = V[0] (the reference's pos-0 case)
     rng = np.random.default_rng(3)
@@ -142,7 +142,9 @@ def test_single_position_returns_v(oracle_mod, kv_type):
     pt = np.array([[1]], np.int32)
     assert kvh.append(k, v, np.zeros(1, np.int32), np.zeros(1, np.int32), pt) == 0
     q = rng.standard_normal((1, Hq, hd)).astype(np.float32)
-    if kv_type == 1:
+    if kv_type == 0:
+        vq = v
+    elif kv_type == 1:
         vq = v.astype(np.float16).astype(np.float32)
     else:
         vq = oracle_mod.dequantize_q8_0(oracle_mod.quantize_q8_0(v))
@@ -176,13 +178,14 @@ def test_gqa_head_map_closed_form(oracle_mod):
         np.testing.assert_allclose(o[0, h], h // (Hq // Hkv) + 1, rtol=0, atol=1e-6)
 
 
-def test_uniform_weights_give_mean(oracle_mod):
+@pytest.mark.parametrize("kv_type", [0, 1])
+def test_uniform_weights_give_mean(oracle_mod, kv_type):
     # identical keys, or q == 0, => softmax uniform => O = mean(V)
     rng = np.random.default_rng(5)
     Hq, Hkv, hd, n = 4, 4, 32, 90
     k = np.broadcast_to(rng.standard_normal((1, Hkv, hd)).astype(np.float32), (n, Hkv, hd)).copy()
-    kvh, pt, _, v = _filled(oracle_mod, rng, Hkv, hd, n, k=k)
-    vq = v.astype(np.float16).astype(np.float64)
+    kvh, pt, _, v = _filled(oracle_mod, rng, Hkv, hd, n, k=k, kv_type=kv_type)
+    vq = (v if kv_type == 0 else v.astype(np.float16)).astype(np.float64)
     q = rng.standard_normal((1, Hq, hd)).astype(np.float32)
     o = kvh.attention(q, Hq, pt, np.array([n], np.int32), mode=oracle_mod.EXACT)
     np.testing.assert_allclose(o[0], vq.mean(0), atol=1e-6)
@@ -264,3 +267,18 @@ def test_missing_page_is_reported(oracle_mod):
     q = rng.standard_normal((1, 4, 32)).astype(np.float32)
     with pytest.raises(RuntimeError):
         kvh.attention(q, 4, bad, np.array([64], np.int32))
+
+
+def test_f32_cache_ggml_mode_is_exact_to_f32_rounding(oracle_mod):
+    # an F32 cache has no operand conversion in ggml (the vec_dot_type of F32
+    # is F32): the ggml-semantics reading equals the float64 one up to f32
+    # accumulation rounding, far inside the parity bar; a stray f16 rounding
+    # of Q, K, P or V (2^-11 relative) would fail it
+    rng = np.random.default_rng(21)
+    Hq, Hkv, hd, n = 8, 2, 128, 700
+    kvh, pt, _, _ = _filled(oracle_mod, rng, Hkv, hd, n, kv_type=0)
+    q = rng.standard_normal((1, Hq, hd)).astype(np.float32)
+    sl = np.array([n], np.int32)
+    gg = kvh.attention(q, Hq, pt, sl, mode=oracle_mod.GGML)
+    ex = kvh.attention(q, Hq, pt, sl, mode=oracle_mod.EXACT)
+    assert_close(gg, ex, max_abs=2e-6, rel_l2=1e-6, what="f32 ggml vs exact")
