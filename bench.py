@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 METRIC = "decode-attn µs/layer-token + HBM GB/s % peak; prefill MFMA util (Mixtral GQA)"
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense f16/bf16
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense f32 matrix
 
 N_LAYER, HQ, HKV, HD, PAGE = 32, 32, 8, 128, 256
 
@@ -179,18 +180,21 @@ def with_traffic(roofline: dict, key: str) -> dict:
     return roofline
 
 
+KV_NAMES = {0: "f32", 1: "f16", 8: "Q8_0"}
+
+
 def decode_leg(torch, key, lens, kv_type, steps, warmup, seed):
-    """One decode workload: lens (one entry per sequence), f16 or Q8_0."""
+    """One decode workload: lens (one entry per sequence), f32, f16 or Q8_0."""
     kv, pt, t_pt, q, seq_len = build_decode_workload(torch, lens, seed, kv_type=kv_type)
     mx = int(max(lens))
     ms, _, k_mean, _, _ = time_decode(torch, kv, t_pt, q, seq_len, mx, steps, warmup)
-    row = HD * 2 if kv_type == 1 else HD // 32 * 34
+    row = {0: HD * 4, 1: HD * 2, 8: HD // 32 * 34}[kv_type]
     alg = 2 * sum(lens) * HKV * row + len(lens) * HQ * HD * 4 * 2
     us_layer = ms * 1e3 / N_LAYER
     ach = alg / (k_mean * 1e-6) / 1e9
-    kname = "decode_f16_kernel<128,4>" if kv_type == 1 else "decode_q8_kernel<128,4>"
+    kname = {0: "decode_f32_kernel<128,4>", 1: "decode_f16_kernel<128,4>", 8: "decode_q8_kernel<128,4>"}[kv_type]
     res = {
-        "workload": f"decode-attn {'f16' if kv_type == 1 else 'Q8_0'} KV, Mixtral GQA 32q/8kv hd128, "
+        "workload": f"decode-attn {KV_NAMES[kv_type]} KV, Mixtral GQA 32q/8kv hd128, "
                     f"B={len(lens)}, context {lens if len(lens) > 1 else lens[0]}, 256-token pages "
                     f"shuffled, {N_LAYER} layers with distinct caches",
         "us_per_layer_step": round(us_layer, 3),
@@ -238,17 +242,17 @@ def copy_ceiling(torch) -> dict:
             "what": "2 GiB device copy (read + write bytes), torch"}
 
 
-def prefill_bench(torch, steps: int, warmup: int, seed: int):
+def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1):
     """Chunked causal prefill: 2048 tokens at positions 2048..4095 over a
-    4096-position paged f16 cache, 32 layers with distinct caches."""
+    4096-position paged f16 (or f32) cache, 8 layers with distinct caches."""
     from strataflow_amd import synth
-    from strataflow_amd.paged_kv import PagedKV, SFA_KV_F16
+    from strataflow_amd.paged_kv import PagedKV
     dev = torch.device("cuda:0")
     n_cached, T = 2048, 2048
     n_kv = n_cached + T
-    n_layer = 8  # distinct caches per step (8 x 16.8 MB)
+    n_layer = 8  # distinct caches per step (8 x 16.8 MB at f16)
     pool_pages = n_kv // PAGE + 4
-    kv = PagedKV(n_layer, HQ, HKV, HD, SFA_KV_F16, PAGE, pool_pages, device=dev)
+    kv = PagedKV(n_layer, HQ, HKV, HD, kv_type, PAGE, pool_pages, device=dev)
     rng = np.random.default_rng(seed)
     pt = torch.from_numpy(synth.page_tables(rng, [n_kv], PAGE, pool_pages)[0]).to(dev)
     gen = torch.Generator(device=dev)
@@ -286,16 +290,28 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int):
     pairs = sum(n_cached + i + 1 for i in range(T))          # causal (q, k) pairs per head
     flops = 4.0 * HD * pairs * HQ                            # QK^T + PV
     tflops = flops / (us * 1e-6) / 1e12
+    peak = MFMA_F16_PEAK_TFLOPS if kv_type == 1 else MFMA_F32_PEAK_TFLOPS
+    name = KV_NAMES[kv_type]
     return {
-        "workload": "causal prefill f16 KV, 2048-token chunk on 2048 cached, Mixtral GQA 32q/8kv hd128",
+        "workload": f"causal prefill {name} KV, 2048-token chunk on 2048 cached, Mixtral GQA 32q/8kv hd128",
         "us_per_layer_chunk": round(us, 2),
         "us_per_layer_token": round(us / T, 5),
         "tflops": round(tflops, 1),
         "roofline": with_traffic({"bound": "mfma", "achieved": round(tflops, 1),
-                                  "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                  "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
-                                  "kernel": "prefill_f16_kernel<128,4>"}, "prefill_2048_on_2048"),
+                                  "peak": peak, "unit": "TFLOP/s",
+                                  "frac": round(tflops / peak, 4), "traffic": None,
+                                  "kernel": f"prefill_{name}_kernel<128,4>"},
+                                 "prefill_2048_on_2048" if kv_type == 1 else "prefill_f32_2048_on_2048"),
         "flop_per_layer_chunk": flops,
+    }
+
+
+def f32_bench(torch, steps: int, warmup: int, seed: int):
+    """F32 KV, the reference's own cache type: decode at context 4096 (B=1,
+    32 layers) and the 2048-on-2048 chunked prefill, both on f32 MFMA."""
+    return {
+        "decode_ctx4096": decode_leg(torch, "decode_f32_ctx4096", [4096], 0, steps, warmup, seed),
+        "prefill_2048_on_2048": prefill_bench(torch, max(steps // 10, 3), 2, seed + 1, kv_type=0),
     }
 
 
@@ -524,7 +540,8 @@ def main():
     ap.add_argument("--no-window", action="store_true", help="skip the KV-window paging legs")
     ap.add_argument("--no-32k", action="store_true", help="skip the f16 context-32768 decode leg")
     ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE + append leg")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope"],
+    ap.add_argument("--no-f32", action="store_true", help="skip the F32-cache legs")
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope", "f32"],
                     help="run one leg only and print its JSON (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
@@ -554,6 +571,7 @@ def main():
 
     if args.only == "decode4k":
         args.no_prefill = args.no_q8 = args.no_window = args.no_32k = args.no_cpu = args.no_rope = True
+        args.no_f32 = True
     if args.only and args.only != "decode4k":
         if args.only == "decode32k":
             r = decode_leg(torch, "decode_f16_ctx32k", [32768], 1, max(args.steps // 4, 5), 3, args.seed + 4)
@@ -563,6 +581,8 @@ def main():
             r = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1)
         elif args.only == "rope":
             r = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
+        elif args.only == "f32":
+            r = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
         else:
             r = window_bench(torch, args.seed + 3)
         print(json.dumps({args.only: r}))
@@ -617,6 +637,8 @@ def main():
         result["window"] = window_bench(torch, args.seed + 3)
     if not args.no_rope:
         result["rope_append"] = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
+    if not args.no_f32:
+        result["f32"] = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
     result["hbm_copy_ceiling"] = copy_ceiling(torch)
     if not args.no_cpu:
         threads, res = cpu_baseline(kv, pt, q[0], ctx)
