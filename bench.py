@@ -213,11 +213,13 @@ def decode_leg(torch, key, lens, kv_type, steps, warmup, seed):
 
 def q8_bench(torch, steps, warmup, seed):
     """Q8_0 KV decode: (a) batch 1 at context 32768; (b) batch 8 with lengths
-    uniform in [8192, 32768] sharing one page pool."""
+    uniform in [8192, 32768] sharing one page pool; and the 2048-on-2048 chunked
+    prefill over a Q8_0 cache."""
     lens_b8 = [int(x) for x in np.random.default_rng(seed).integers(8192, 32769, 8)]
     return {
         "ctx32k_b1": decode_leg(torch, "decode_q8_0_ctx32k_b1", [32768], 8, steps, warmup, seed),
         "b8_varlen_8k_32k": decode_leg(torch, "decode_q8_0_b8", lens_b8, 8, steps, warmup, seed),
+        "prefill_2048_on_2048": prefill_bench(torch, max(steps // 3, 3), 2, seed + 1, kv_type=8),
     }
 
 
@@ -290,7 +292,8 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1):
     pairs = sum(n_cached + i + 1 for i in range(T))          # causal (q, k) pairs per head
     flops = 4.0 * HD * pairs * HQ                            # QK^T + PV
     tflops = flops / (us * 1e-6) / 1e12
-    peak = MFMA_F16_PEAK_TFLOPS if kv_type == 1 else MFMA_F32_PEAK_TFLOPS
+    # f32: the f32 MFMA peak; Q8_0 (int8 QK, f16 PV): the f16 peak, the slower of its two
+    peak = MFMA_F32_PEAK_TFLOPS if kv_type == 0 else MFMA_F16_PEAK_TFLOPS
     name = KV_NAMES[kv_type]
     return {
         "workload": f"causal prefill {name} KV, 2048-token chunk on 2048 cached, Mixtral GQA 32q/8kv hd128",
@@ -300,8 +303,10 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1):
         "roofline": with_traffic({"bound": "mfma", "achieved": round(tflops, 1),
                                   "peak": peak, "unit": "TFLOP/s",
                                   "frac": round(tflops / peak, 4), "traffic": None,
-                                  "kernel": f"prefill_{name}_kernel<128,4>"},
-                                 "prefill_2048_on_2048" if kv_type == 1 else "prefill_f32_2048_on_2048"),
+                                  "kernel": {0: "prefill_f32_kernel<128,4>", 1: "prefill_f16_kernel<128,4>",
+                                             8: "prefill_q8_kernel<128,4>"}[kv_type]},
+                                 {1: "prefill_2048_on_2048", 0: "prefill_f32_2048_on_2048",
+                                  8: "prefill_q8_0_2048_on_2048"}[kv_type]),
         "flop_per_layer_chunk": flops,
     }
 

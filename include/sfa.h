@@ -179,8 +179,8 @@ SFA_API int sfa_attn_decode_merge(const sfa_kv_desc *kv, const float *q, float *
  * q_pos0 .. q_pos0+T-1, whose K/V are already appended.  Token t attends kv
  * positions kv_lo .. q_pos0+t (causal -INF mask above the diagonal, the
  * llama.cpp kq_mask convention).  q: [T][n_head][head_dim] f32,
- * out: [T][n_head * head_dim] f32.  F32 and F16 caches (a Q8_0 cache returns
- * SFA_ERR_UNSUPPORTED). */
+ * out: [T][n_head * head_dim] f32.  F32, F16 and Q8_0 caches (Q8_0 with
+ * head_dim >= 64, as in decode). */
 SFA_API int sfa_attn_prefill(const sfa_kv_desc *kv, const float *q, float *out,
                              const int32_t *page_table, int32_t max_pages,
                              int32_t q_pos0, int32_t T, int32_t kv_lo,

@@ -91,7 +91,7 @@ SFA_API int sfa_pager_rope_append(sfa_pager *pager, int32_t layer, float *q, con
  * f32 device, out [n_tokens][n_head * head_dim] f32 device.  A step with one
  * token per sequence runs sfa_attn_decode over the batch (split plan sized for
  * n_ctx when lossless, `window` when windowed); other steps run
- * sfa_attn_prefill per sequence (lossless F32 and F16 caches only). */
+ * sfa_attn_prefill per sequence (lossless only; Q8_0 needs head_dim >= 64). */
 SFA_API int sfa_pager_attend(sfa_pager *pager, int32_t layer, const float *q, float *out,
                              void *stream);
 

@@ -497,11 +497,307 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
     }
 }
 
+// Q8_0 cache (head_dim 64 or 128), ggml's arithmetic: Q is quantised to Q8_0
+// (d = amax/127 stored fp16, q = round(x/d)), S^T = K * Q^T runs on
+// v_mfma_i32_32x32x32_i8 one 32-dim block at a time and s += float(sumi) *
+// (d_k * d_q) in block order (ggml_vec_dot_q8_0_q8_0); V is dequantised to f16
+// (q * d rounded once) into the f16 kernel's V tile, and the softmax and P*V
+// are the f16 kernel's.  Tiles are staged through registers: one thread per
+// (position, block) loads the 34-byte block (and the V block) as 4-aligned
+// dwords, then writes the quants to a 16-byte-aligned K tile (chunks XOR-
+// swizzled by row), the scale to a per-block scale row, and the dequantised V.
+template <int HD, int G>
+__global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
+    static_assert(HD == 64 || HD == 128, "head_dim");
+    constexpr int NB = HD / 32;           // blocks per row
+    constexpr int DB = HD / 32;
+    constexpr int QB = 128 / G;
+    constexpr int ROW = HD * 2 + 64;      // padded f16 V row (bytes)
+    constexpr int QROW = HD;              // int8 K row in LDS (bytes)
+    constexpr int SW = QROW / 16 - 1;     // K chunk swizzle mask
+    constexpr int RB = NB * kQ8Bytes;     // bytes of one cache row
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * QROW];
+    __shared__ __attribute__((aligned(16))) _Float16 lds_dk[2][NB][kPBN];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kPBN * ROW];
+
+    const int kvh = (int)blockIdx.x % p.n_head_kv;
+    const int qblk = p.n_qblk - 1 - (int)blockIdx.x / p.n_head_kv;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+    const int64_t col_bytes = (int64_t)p.n_head_kv * RB;
+
+    const int rho = wave * 32 + n;
+    const int g = rho / QB;
+    const int tq = qblk * QB + rho % QB;
+    const bool row_ok = tq < p.T;
+    const int h = kvh * G + g;
+    const int qp = p.q_pos0 + tq;
+
+    const int first_tok = qblk * QB;
+    int last_tok = first_tok + QB - 1;
+    if (last_tok > p.T - 1) last_tok = p.T - 1;
+    const int kv_hi = p.q_pos0 + last_tok;
+    const int q_lo = p.q_pos0 + first_tok;
+    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
+    const int tile0 = lo / kPBN;
+    const int tile1 = kv_hi / kPBN;
+    const bool block_full = (qblk + 1) * QB <= p.T;
+
+    // staging unit of this thread: position sp_, block sc (threads past
+    // kPBN * NB stage nothing)
+    const bool stager = tid < kPBN * NB;
+    const int sp_ = tid / NB, sc = tid % NB;
+    uint32_t kraw[9], vraw[9];
+    bool page_ok = false;
+    auto load = [&](int t) {
+        const int pos0 = t * kPBN;
+        const int lp = pos0 / p.page_size;
+        const int32_t pid = __builtin_amdgcn_readfirstlane(lp < p.max_pages ? p.page_table[lp] : -1);
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        page_ok = kb != nullptr && vb != nullptr;
+        if (!page_ok || !stager) return;
+        // the 36 bytes at or 2 below the block (rows are 4-byte aligned)
+        const int64_t off = (int64_t)(pos0 - lp * p.page_size + sp_) * col_bytes + (int64_t)kvh * RB +
+                            kQ8Bytes * sc - (sc & 1) * 2;
+        const intx4 k0 = load16_a4(kb + off), k1 = load16_a4(kb + off + 16);
+        const intx4 v0 = load16_a4(vb + off), v1 = load16_a4(vb + off + 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kraw[j] = (uint32_t)k0[j]; kraw[4 + j] = (uint32_t)k1[j];
+            vraw[j] = (uint32_t)v0[j]; vraw[4 + j] = (uint32_t)v1[j];
+        }
+        kraw[8] = load4_a4(kb + off + 32);
+        vraw[8] = load4_a4(vb + off + 32);
+    };
+    // registers -> LDS buffer: K quants (swizzled 16-byte chunks 2sc, 2sc+1 of
+    // row sp_), its scale, and V dequantised (rows outside [lo, kv_hi] zero)
+    auto store = [&](int t, int buf) {
+        if (!stager) return;
+        const int pos0 = t * kPBN;
+        uint32_t kq[8], vq[8];
+        uint32_t kd, vd;
+        if ((sc & 1) == 0) {
+            kd = kraw[0] & 0xffffu;
+            vd = vraw[0] & 0xffffu;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                kq[j] = __builtin_amdgcn_alignbyte(kraw[j + 1], kraw[j], 2);
+                vq[j] = __builtin_amdgcn_alignbyte(vraw[j + 1], vraw[j], 2);
+            }
+        } else {
+            kd = kraw[0] >> 16;
+            vd = vraw[0] >> 16;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                kq[j] = kraw[j + 1];
+                vq[j] = vraw[j + 1];
+            }
+        }
+        if (!page_ok) {
+            kd = 0u;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) kq[j] = 0u;
+        }
+        uint8_t *krow = &lds_k[buf][sp_ * QROW];
+        *reinterpret_cast<intx4 *>(krow + 16 * ((2 * sc) ^ (sp_ & SW))) =
+            intx4{(int)kq[0], (int)kq[1], (int)kq[2], (int)kq[3]};
+        *reinterpret_cast<intx4 *>(krow + 16 * ((2 * sc + 1) ^ (sp_ & SW))) =
+            intx4{(int)kq[4], (int)kq[5], (int)kq[6], (int)kq[7]};
+        lds_dk[buf][sc][sp_] = __builtin_bit_cast(_Float16, (uint16_t)kd);
+        // q * d rounded to f16 on packed halves, as in the Q8_0 decode kernel
+        const bool ok = page_ok && pos0 + sp_ >= lo && pos0 + sp_ <= kv_hi;
+        const _Float16 dv = ok ? __builtin_bit_cast(_Float16, (uint16_t)vd) : (_Float16)0.0f;
+        const half2v dv2 = {dv, dv};
+        const half2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        half8 hv[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t x = vq[j] ^ 0x80808080u;
+            const half2v a = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) + bias) * dv2;
+            const half2v b = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) + bias) * dv2;
+            hv[j >> 1][4 * (j & 1) + 0] = a[0];
+            hv[j >> 1][4 * (j & 1) + 1] = a[1];
+            hv[j >> 1][4 * (j & 1) + 2] = b[0];
+            hv[j >> 1][4 * (j & 1) + 3] = b[1];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            *reinterpret_cast<half8 *>(&lds_v[buf][sp_ * ROW + 64 * sc + 16 * k]) = hv[k];
+    };
+
+    load(tile0);
+
+    // Q8_0 of this lane's query row: block c, elements 16hh .. 16hh+15 (the
+    // B operand), d_q = fp16(amax / 127) as f32; rows past T quantise zeros
+    intx4 qa[NB];
+    float dq[NB];
+    {
+        const float *qr = p.q + ((int64_t)(row_ok ? tq : 0) * p.n_head + h) * HD;
+        floatx4 xr[NB][4];
+#pragma unroll
+        for (int c = 0; c < NB; ++c)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xr[c][j] = reinterpret_cast<const floatx4 *>(qr + 32 * c + 16 * hh)[j];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            float x[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x[4 * j] = row_ok ? xr[c][j][0] : 0.0f;
+                x[4 * j + 1] = row_ok ? xr[c][j][1] : 0.0f;
+                x[4 * j + 2] = row_ok ? xr[c][j][2] : 0.0f;
+                x[4 * j + 3] = row_ok ? xr[c][j][3] : 0.0f;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(x[j]));
+            amax = fmaxf(amax, xor32(amax));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int q0 = (int)roundf(x[4 * j] * id), q1 = (int)roundf(x[4 * j + 1] * id);
+                const int q2 = (int)roundf(x[4 * j + 2] * id), q3 = (int)roundf(x[4 * j + 3] * id);
+                qa[c][j] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
+            }
+            dq[c] = (float)(_Float16)d;
+        }
+    }
+
+    store(tile0, 0);
+    __syncthreads();
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int gq = lane >> 4, rr = lane & 15;
+    const int tr_off = (4 * (gq >> 1) + (rr >> 2)) * ROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
+    const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    bool ok_cur = page_ok;
+    for (int t = tile0; t <= tile1; ++t) {
+        const int buf = (t - tile0) & 1;
+        const int pos0 = t * kPBN;
+        const bool dead = !ok_cur;
+        if (t < tile1) load(t + 1);  // in flight while this tile computes
+        const uint8_t *kt = lds_k[buf];
+        const uint8_t *vt = lds_v[buf];
+
+        // S^T = K * Q^T block by block, scaled in block order
+        floatx16 s[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+            const int r = 32 * pb + n;
+#pragma unroll
+            for (int c = 0; c < NB; ++c) {
+                const intx4 a = *reinterpret_cast<const intx4 *>(kt + r * QROW + 16 * ((2 * c + hh) ^ (r & SW)));
+                const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qa[c], intx16{}, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // d_k of positions 32pb + 8j + 4hh + 0..3
+                    const half4 dk4 = *reinterpret_cast<const half4 *>(&lds_dk[buf][c][32 * pb + 8 * j + 4 * hh]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        s[pb][4 * j + e] += (float)acc[4 * j + e] * ((float)dk4[e] * dq[c]);
+                }
+            }
+        }
+        const bool edge = dead || pos0 < lo || pos0 + kPBN - 1 > q_lo || !block_full;
+        if (edge) {
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
+                    s[pb][i] = (!dead && row_ok && kp >= lo && kp <= qp) ? s[pb][i] : -INFINITY;
+                }
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
+        mt = fmaxf(mt, xor32(mt)) * p.scale_log2;
+        float alpha = 1.0f;
+        if (mt > m_run + kRescaleLog2) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mt);
+            m_run = mt;
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        half8 pbv[2][2];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                pbv[pb][i >> 3][i & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[pb][i], p.scale_log2, -m_use));
+        }
+        float ls = 0.0f;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(HalfPairs, pbv[pb][kk]).v[j], ones, ls, false);
+        l_run = l_run * alpha + ls;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d) o[d] *= alpha;
+        }
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                half8 va[DB];
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const half4 hv = tr16_read(vt + tr_off + (32 * pb + 16 * kk + 8 * u) * ROW + 64 * d);
+                        va[d][4 * u + 0] = hv[0];
+                        va[d][4 * u + 1] = hv[1];
+                        va[d][4 * u + 2] = hv[2];
+                        va[d][4 * u + 3] = hv[3];
+                    }
+                }
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d], pbv[pb][kk], o[d], 0, 0, 0);
+            }
+        }
+        ok_cur = page_ok;  // the loaded (next) tile's page status
+        if (t < tile1) store(t + 1, buf ^ 1);
+        __syncthreads();
+    }
+
+    l_run += xor32(l_run);
+    if (row_ok) {
+        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+        float *orow = p.out + ((int64_t)tq * p.n_head + h) * HD;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                orow[32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i] * inv;
+            }
+        }
+    }
+}
+
 template <int HD, int G>
 static void launch_prefill(const PrefillParams &p, int kv_type, hipStream_t s) {
-    if (kv_type == SFA_KV_F32)
+    if (kv_type == SFA_KV_F32) {
         hipLaunchKernelGGL((prefill_f32_kernel<HD, G>), dim3(p.n_qblk * p.n_head_kv), dim3(256), 0, s, p);
-    else
+    } else if (kv_type == SFA_KV_Q8_0) {
+        if constexpr (HD >= 64)
+            hipLaunchKernelGGL((prefill_q8_kernel<HD, G>), dim3(p.n_qblk * p.n_head_kv), dim3(256), 0, s, p);
+    } else
         hipLaunchKernelGGL((prefill_f16_kernel<HD, G>), dim3(p.n_qblk * p.n_head_kv), dim3(256), 0, s, p);
 }
 
@@ -519,7 +815,9 @@ static int launch_prefill_g(const PrefillParams &p, int G, int kv_type, hipStrea
 int prefill_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
                    int32_t max_pages, int32_t q_pos0, int32_t T, int32_t kv_lo, float scale,
                    hipStream_t stream) {
-    if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_F32) return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_F32 && kv->kv_type != SFA_KV_Q8_0)
+        return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type == SFA_KV_Q8_0 && kv->head_dim < 64) return SFA_ERR_UNSUPPORTED;
     if (kv->page_size % kPBN != 0) return SFA_ERR_UNSUPPORTED;
     if (q == nullptr || out == nullptr || page_table == nullptr) return SFA_ERR_INVALID_ARGUMENT;
     if (T < 0 || q_pos0 < 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;

@@ -150,7 +150,7 @@ def test_pager_window_matches_oracle(gpu, oracle_mod):
     assert_close(out.cpu().numpy(), ref, what="window paged vs oracle")
 
 
-@pytest.mark.parametrize("kv_type", [SFA_KV_F32, SFA_KV_F16])
+@pytest.mark.parametrize("kv_type", [SFA_KV_F32, SFA_KV_F16, SFA_KV_Q8_0])
 def test_pager_prefill_chunk_over_cold_pages(gpu, oracle_mod, kv_type):
     # a 200-token chunk whose history is partly in the cold pool
     host = oracle_mod.HostPagedKv(8, 128, 256, kv_type, 2 * 16 + 2)

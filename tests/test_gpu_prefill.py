@@ -123,6 +123,12 @@ def test_prefill_rejects_unsupported(gpu, oracle_mod):
     d32.page_size = 32
     assert lib.sfa_attn_prefill(ctypes.byref(d32), tq.data_ptr(), out.data_ptr(), tpt.data_ptr(),
                                 int(pt.shape[1]), 10, 5, 0, 0.17, s) == _lib.SFA_ERR_UNSUPPORTED
+    # a Q8_0 cache needs head_dim >= 64 (two 16-byte halves per block per lane)
+    d8 = _lib.SfaKvDesc()
+    ctypes.memmove(ctypes.byref(d8), ctypes.byref(d), ctypes.sizeof(d))
+    d8.kv_type = 8
+    assert lib.sfa_attn_prefill(ctypes.byref(d8), tq.data_ptr(), out.data_ptr(), tpt.data_ptr(),
+                                int(pt.shape[1]), 10, 5, 0, 0.17, s) == _lib.SFA_ERR_UNSUPPORTED
     # T == 0 is a no-op
     assert lib.sfa_attn_prefill(ctypes.byref(d), tq.data_ptr(), out.data_ptr(), tpt.data_ptr(),
                                 int(pt.shape[1]), 10, 0, 0, 0.17, s) == _lib.SFA_OK
@@ -163,3 +169,66 @@ def test_prefill_f32_rows_equal_f32_decode(gpu, oracle_mod):
     sl = torch.tensor([n_cached + t + 1 for t in rows], dtype=torch.int32, device=gpu)
     dec = dev.decode(0, tq, tpt, sl, n_kv).cpu().numpy().reshape(len(rows), -1)
     assert_close(out[rows], dec, max_abs=F32_MAX_ABS, rel_l2=F32_REL, what="f32 prefill rows vs decode")
+
+
+# ---- Q8_0 cache: ggml's integer block dots (Q quantised to Q8_0), V
+# dequantised to f16; gated against the ggml-semantics oracle at the parity bar
+Q8_EXACT_ABS, Q8_EXACT_REL = 2e-2, 2e-2  # vs float64: the Q quantisation error
+
+
+def test_prefill_q8_golden(gpu, oracle_mod):
+    import torch
+    from strataflow_amd.paged_kv import PagedKV
+    g = golden("attn_q8_gqa2_prefill")
+    n_kv, Hkv = g["k_q8"].shape[:2]
+    hd = g["k_q8"].shape[2] // 34 * 32
+    Hq, T = int(g["n_head"]), g["q"].shape[0]
+    ps, n_pages = 64, (n_kv + 63) // 64 + 2
+    kp, pt = scatter_columns(g["k_q8"].reshape(n_kv, -1), ps, n_pages, np.random.default_rng(3))
+    vp, _ = scatter_columns(g["v_q8"].reshape(n_kv, -1), ps, n_pages, np.random.default_rng(3))
+    dev = PagedKV(1, Hq, Hkv, hd, 8, ps, n_pages, device=gpu)
+    dev.k[0].copy_(torch.from_numpy(kp))
+    dev.v[0].copy_(torch.from_numpy(vp))
+    q_pos0 = int(g["qpos"][0])
+    out = dev.prefill(0, torch.from_numpy(g["q"]).to(gpu), torch.from_numpy(pt[0]).to(gpu), q_pos0,
+                      int(g["kv_lo"]), scale=float(g["scale"]))
+    out = out.cpu().numpy().reshape(g["exact"].shape)
+    assert_close(out, g["ggml"], what="q8 prefill vs ggml golden")
+    assert_close(out, g["exact"], max_abs=Q8_EXACT_ABS, rel_l2=Q8_EXACT_REL, what="q8 prefill vs exact golden")
+
+
+@pytest.mark.parametrize("shape,n_cached,T,kv_lo,page_size", [
+    ((32, 8, 128), 300, 256, 0, 256),
+    ((8, 8, 64), 70, 130, 0, 128),
+    ((16, 8, 64), 333, 97, 77, 128),     # unaligned window start
+    ((32, 4, 128), 129, 260, 0, 512),    # g = 8
+    ((16, 16, 128), 1000, 64, 0, 64),    # g = 1, smallest page the tiles allow
+    ((8, 4, 64), 0, 1, 0, 64),           # one token, no history
+])
+def test_prefill_q8_vs_oracle(gpu, oracle_mod, shape, n_cached, T, kv_lo, page_size):
+    Hq, Hkv, hd = shape
+    host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=Hq, Hkv=Hkv, hd=hd, n_cached=n_cached, T=T,
+                                   page_size=page_size, seed=T + hd + 8, kv_type=8)
+    out = run(dev, gpu, pt, q, n_cached, kv_lo)
+    ref = host.attention(q[None], Hq, pt, np.array([n_kv], np.int32), np.array([kv_lo], np.int32),
+                         T=T, mode=oracle_mod.GGML)[0].reshape(T, -1)
+    assert_close(out, ref, what=f"q8 {shape} T={T} vs ggml")
+    ex = host.attention(q[None], Hq, pt, np.array([n_kv], np.int32), np.array([kv_lo], np.int32),
+                        T=T, mode=oracle_mod.EXACT)[0].reshape(T, -1)
+    assert_close(out, ex, max_abs=Q8_EXACT_ABS, rel_l2=Q8_EXACT_REL, what=f"q8 {shape} T={T} vs exact")
+
+
+def test_prefill_q8_rows_match_q8_decode(gpu, oracle_mod):
+    # a causal prefill row and the Q8_0 decode at its position share the
+    # integer QK arithmetic; they differ only in P*V accumulation order
+    import torch
+    Hq, Hkv, hd, n_cached, T = 32, 8, 128, 700, 150
+    host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=Hq, Hkv=Hkv, hd=hd, n_cached=n_cached, T=T,
+                                   seed=19, kv_type=8)
+    out = run(dev, gpu, pt, q, n_cached)
+    rows = [0, 1, 63, 64, 149]
+    tq = torch.from_numpy(q[rows]).to(gpu)
+    tpt = torch.from_numpy(np.repeat(pt, len(rows), axis=0)).to(gpu)
+    sl = torch.tensor([n_cached + t + 1 for t in rows], dtype=torch.int32, device=gpu)
+    dec = dev.decode(0, tq, tpt, sl, n_kv).cpu().numpy().reshape(len(rows), -1)
+    assert_close(out[rows], dec, max_abs=1e-3, rel_l2=5e-4, what="q8 prefill rows vs decode")
