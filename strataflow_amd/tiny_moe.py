@@ -153,14 +153,15 @@ class TinyMoe:
 
 
 class HipAttention:
-    """The attention node on the GPU through libsfa.so: per layer a paged f16
-    cache (one 256-token page per sequence here), sfa_kv_append, then
-    sfa_attn_decode (one token) or sfa_attn_prefill (a chunk).  With
-    ``fused_rope`` it receives Q and K before RoPE and runs sfa_rope_kv_append
-    (RoPE of Q and K fused with the append) instead."""
+    """The attention node on the GPU through libsfa.so: per layer a paged cache
+    (f16 by default, or f32 as the reference keeps it; one 256-token page per
+    sequence here), sfa_kv_append, then sfa_attn_decode (one token) or
+    sfa_attn_prefill (a chunk).  With ``fused_rope`` it receives Q and K before
+    RoPE and runs sfa_rope_kv_append (RoPE of Q and K fused with the append)
+    instead."""
 
     def __init__(self, cfg: TinyMoeConfig, n_ctx: int, device: str = "cuda", seed: int = 0,
-                 fused_rope: bool = False):
+                 fused_rope: bool = False, kv_type: int | None = None):
         self.applies_rope = fused_rope
         import torch
 
@@ -168,8 +169,9 @@ class HipAttention:
         self.torch, self.cfg, self.n_ctx = torch, cfg, n_ctx
         max_pages = (n_ctx + cfg.page_size - 1) // cfg.page_size
         n_pages = max_pages + 3
-        self.kv = PagedKV(cfg.n_layer, cfg.n_head, cfg.n_head_kv, cfg.head_dim, SFA_KV_F16,
-                          cfg.page_size, n_pages, device=device)
+        self.kv = PagedKV(cfg.n_layer, cfg.n_head, cfg.n_head_kv, cfg.head_dim,
+                          SFA_KV_F16 if kv_type is None else kv_type, cfg.page_size, n_pages,
+                          device=device)
         rng = np.random.default_rng(seed)
         self.pt = torch.from_numpy(synth.page_tables(rng, [n_ctx], cfg.page_size, n_pages,
                                                      max_pages)).to(device)

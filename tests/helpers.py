@@ -120,15 +120,16 @@ class Case:
 
 class OracleAttention:
     """The attention node on the CPU oracle, with the call shape of
-    strataflow_amd.tiny_moe.HipAttention: per layer a host paged f16 cache,
-    append at pos0.., attention of the T new tokens (causal)."""
+    strataflow_amd.tiny_moe.HipAttention: per layer a host paged cache (f16 by
+    default), append at pos0.., attention of the T new tokens (causal)."""
 
-    def __init__(self, oracle_mod, cfg, n_ctx: int, mode: int):
+    def __init__(self, oracle_mod, cfg, n_ctx: int, mode: int, kv_type: int | None = None):
         self.o, self.cfg, self.mode = oracle_mod, cfg, mode
         n_pages = (n_ctx + cfg.page_size - 1) // cfg.page_size
         self.pt = np.arange(n_pages, dtype=np.int32)[None]
-        self.host = [oracle_mod.HostPagedKv(cfg.n_head_kv, cfg.head_dim, cfg.page_size,
-                                            oracle_mod.KV_F16, n_pages) for _ in range(cfg.n_layer)]
+        kt = oracle_mod.KV_F16 if kv_type is None else kv_type
+        self.host = [oracle_mod.HostPagedKv(cfg.n_head_kv, cfg.head_dim, cfg.page_size, kt, n_pages)
+                     for _ in range(cfg.n_layer)]
 
     def __call__(self, layer, q, k, v, pos0):
         T = q.shape[0]

@@ -40,18 +40,20 @@ def test_tiny_moe_oracle_modes_agree(oracle_mod):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kv_type", [1, 0], ids=["f16_cache", "f32_cache"])
 @pytest.mark.parametrize("fused_rope", [False, True], ids=["host_rope", "fused_rope_append"])
 @pytest.mark.parametrize("chunked", [False, True], ids=["per_token_prompt", "chunked_prompt"])
-def test_tiny_moe_greedy_identical(gpu, oracle_mod, chunked, fused_rope):
+def test_tiny_moe_greedy_identical(gpu, oracle_mod, chunked, fused_rope, kv_type):
+    # the f16 cache is the config's; f32 is the reference engine's own cache type
     cfg = TinyMoeConfig()
     w = TinyMoeWeights(cfg, seed=0)
     n_ctx = N_PROMPT + N_GEN
-    ref = TinyMoe(cfg, w, OracleAttention(oracle_mod, cfg, n_ctx, oracle_mod.GGML)).generate(
+    ref = TinyMoe(cfg, w, OracleAttention(oracle_mod, cfg, n_ctx, oracle_mod.GGML, kv_type=kv_type)).generate(
         _prompt(cfg), N_GEN, chunked_prompt=chunked)
-    got = TinyMoe(cfg, w, HipAttention(cfg, n_ctx, device=gpu, fused_rope=fused_rope)).generate(
+    got = TinyMoe(cfg, w, HipAttention(cfg, n_ctx, device=gpu, fused_rope=fused_rope, kv_type=kv_type)).generate(
         _prompt(cfg), N_GEN, chunked_prompt=chunked)
     same, dl, margin = _compare(ref, got)
-    print(f"\n[tiny-moe chunked={chunked} fused_rope={fused_rope}] seq match={same} max per-step |dlogit|={dl:.3e} "
-          f"min top-2 margin={margin:.3e} tokens={got[0]}")
+    print(f"\n[tiny-moe kv_type={kv_type} chunked={chunked} fused_rope={fused_rope}] seq match={same} "
+          f"max per-step |dlogit|={dl:.3e} min top-2 margin={margin:.3e} tokens={got[0]}")
     assert same, (ref[0], got[0])
     assert dl < 1e-3
