@@ -40,16 +40,104 @@ struct PrefillParams {
 };
 
 constexpr int kPBN = 64;           // positions per prefill tile
+constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (P <= 2^8)
 struct HalfPairs {
     half2v v[4];  // the four dwords of a half8
 };
-constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (P <= 2^8)
+
+// The workgroup's query block and this lane's query row.  Workgroup L serves
+// kv head L % Hkv and query block n_qblk - 1 - L / Hkv (heaviest blocks first);
+// its 128 MFMA columns (4 waves x 32) are the g heads of that kv head times
+// 128/g tokens, column n of wave w being row 32w + n.
+struct PrefillRows {
+    int kvh, tq, h, qp;   // this lane's row: token, query head, absolute position
+    bool row_ok;          // tq < T
+    int q_lo, kv_hi, lo;  // block's first query position, last attended position, window start
+    int tile0, tile1;     // 64-position tiles of the block's kv range (inclusive)
+    bool block_full;      // every row of the block is < T
+};
+template <int G>
+__device__ __attribute__((always_inline)) inline PrefillRows prefill_rows(const PrefillParams &p, int wave, int n) {
+    constexpr int QB = 128 / G;  // query tokens per workgroup
+    PrefillRows r;
+    r.kvh = (int)blockIdx.x % p.n_head_kv;
+    const int qblk = p.n_qblk - 1 - (int)blockIdx.x / p.n_head_kv;
+    const int rho = wave * 32 + n;
+    r.tq = qblk * QB + rho % QB;
+    r.row_ok = r.tq < p.T;
+    r.h = r.kvh * G + rho / QB;
+    r.qp = p.q_pos0 + r.tq;
+    const int first_tok = qblk * QB;
+    int last_tok = first_tok + QB - 1;
+    if (last_tok > p.T - 1) last_tok = p.T - 1;
+    r.kv_hi = p.q_pos0 + last_tok;
+    r.q_lo = p.q_pos0 + first_tok;
+    r.lo = p.kv_lo > 0 ? p.kv_lo : 0;
+    r.tile0 = r.lo / kPBN;
+    r.tile1 = r.kv_hi / kPBN;
+    r.block_full = (qblk + 1) * QB <= p.T;
+    return r;
+}
+
+// A tile needs masking where it meets the window start, the diagonal or rows
+// past T, or when its page was invalid (wave-uniform).
+__device__ __attribute__((always_inline)) inline bool prefill_edge(const PrefillRows &r, int pos0, bool dead) {
+    return dead || pos0 < r.lo || pos0 + kPBN - 1 > r.q_lo || !r.block_full;
+}
+
+// Scores of positions outside [lo, qp] (all of them for a dead tile or a row
+// past T) -> -inf; register i of block pb is position pos0 + 32pb + 8(i/4) +
+// 4hh + i%4.
+__device__ __attribute__((always_inline)) inline void prefill_mask(floatx16 (&s)[2], const PrefillRows &r, int pos0, int hh, bool dead) {
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
+            s[pb][i] = (!dead && r.row_ok && kp >= r.lo && kp <= r.qp) ? s[pb][i] : -INFINITY;
+        }
+    }
+}
+
+// Row max of the tile (both 32-position blocks, both lane halves) in the log2
+// domain, with the lazy reference: m_run moves only when the tile max exceeds
+// it by 2^8 (P stays <= 256; exact since O and l share the reference).
+// Returns the factor O and l are rescaled by (1 when the reference stays).
+__device__ __attribute__((always_inline)) inline float prefill_rescale(const floatx16 (&s)[2], float scale_log2, float &m_run) {
+    float mt = -INFINITY;
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
+    mt = fmaxf(mt, xor32(mt)) * scale_log2;
+    float alpha = 1.0f;
+    if (mt > m_run + kRescaleLog2) {
+        alpha = __builtin_amdgcn_exp2f(m_run - mt);  // m_run == -inf -> 0
+        m_run = mt;
+    }
+    return alpha;
+}
+
+// O^T / l to the output row of this lane (register i of dim block d is dim
+// 32d + 8(i/4) + 4hh + i%4); l is the lane's half of the row sum.
+template <int HD>
+__device__ __attribute__((always_inline)) inline void prefill_write(const floatx16 (&o)[HD / 32], float l_run, const PrefillRows &r,
+                                     const PrefillParams &p, int hh) {
+    l_run += xor32(l_run);
+    if (!r.row_ok) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    float *orow = p.out + ((int64_t)r.tq * p.n_head + r.h) * HD;
+#pragma unroll
+    for (int d = 0; d < HD / 32; ++d) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) orow[32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i] * inv;
+    }
+}
 
 template <int HD, int G>
 __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     constexpr int KC = HD / 16;
     constexpr int DB = HD / 32;
-    constexpr int QB = 128 / G;           // query tokens per workgroup
     constexpr int ROW = HD * 2 + 64;      // padded LDS row (bytes)
     constexpr int CPR = HD / 8;           // 16-byte chunks per row
     constexpr int CHUNKS = kPBN * CPR;    // 16-byte chunks per tile
@@ -72,7 +160,6 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     // query block of one kv head runs on one XCD and that head's K/V stays in
     // its L2 (each tile is re-read by every query block of the head).
     const int kvh = (int)blockIdx.x % p.n_head_kv;
-    const int qblk = p.n_qblk - 1 - (int)blockIdx.x / p.n_head_kv;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -82,23 +169,10 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     const int64_t col_bytes = (int64_t)Hkv * HD * 2;
 
     // this lane's query row (MFMA column n): head g of the group, token tq
-    const int rho = wave * 32 + n;
-    const int g = rho / QB;
-    const int tq = qblk * QB + rho % QB;
-    const bool row_ok = tq < p.T;
-    const int h = kvh * G + g;
-    const int qp = p.q_pos0 + tq;
-
-    // the block's kv range
-    const int first_tok = qblk * QB;
-    int last_tok = first_tok + QB - 1;
-    if (last_tok > p.T - 1) last_tok = p.T - 1;
-    const int kv_hi = p.q_pos0 + last_tok;     // inclusive
-    const int q_lo = p.q_pos0 + first_tok;     // smallest query position of the block
-    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
-    const int tile0 = lo / kPBN;
-    const int tile1 = kv_hi / kPBN;             // inclusive
-    const bool block_full = (qblk + 1) * QB <= p.T;
+    const PrefillRows rows = prefill_rows<G>(p, wave, n);
+    const bool row_ok = rows.row_ok;
+    const int tq = rows.tq, h = rows.h;
+    const int kv_hi = rows.kv_hi, lo = rows.lo, tile0 = rows.tile0, tile1 = rows.tile1;
 
     // cooperative tile loads into registers: chunk i*256 + tid -> row r =
     // 16i + tid / CPR, 16-byte chunk c = tid % CPR.  Buffer loads: the tile's
@@ -212,32 +286,10 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
             }
         }
         // masking only where the tile meets the window start, the diagonal
-        // or rows past T (wave-uniform branch)
-        const bool edge = pos0 < lo || pos0 + kPBN - 1 > q_lo || !block_full;
-        if (edge) {
-#pragma unroll
-            for (int pb = 0; pb < 2; ++pb) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                    s[pb][i] = (row_ok && kp >= lo && kp <= qp) ? s[pb][i] : -INFINITY;
-                }
-            }
-        }
-        // raw scores; the scale (> 0) is applied inside the exponent
-        float mt = -INFINITY;
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
-        mt = fmaxf(mt, xor32(mt)) * p.scale_log2;
-        // lazy rescale: keep the reference max until the tile max exceeds it
-        // by 2^8 (P stays <= 256, exact since O and l share the reference)
-        float alpha = 1.0f;
-        if (mt > m_run + kRescaleLog2) {
-            alpha = __builtin_amdgcn_exp2f(m_run - mt);  // m_run == -inf -> 0
-            m_run = mt;
-        }
+        // or rows past T (wave-uniform branch); raw scores, the scale (> 0)
+        // is applied inside the exponent
+        if (prefill_edge(rows, pos0, false)) prefill_mask(s, rows, pos0, hh, false);
+        const float alpha = prefill_rescale(s, p.scale_log2, m_run);
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         half8 pbv[2][2];
 #pragma unroll
@@ -289,18 +341,7 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         __syncthreads();
     }
 
-    l_run += xor32(l_run);
-    if (row_ok) {
-        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-        float *orow = p.out + ((int64_t)tq * p.n_head + h) * HD;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                orow[32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i] * inv;
-            }
-        }
-    }
+    prefill_write<HD>(o, l_run, rows, p, hh);
 }
 
 // F32 cache (the reference's own type): ggml converts nothing, so both
@@ -317,7 +358,6 @@ template <int HD, int G>
 __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
     constexpr int KH = HD / 2;           // Q / K floats per lane (half a row)
     constexpr int DB = HD / 32;
-    constexpr int QB = 128 / G;
     constexpr int RB = HD * 4;           // row bytes
     constexpr int CPR = RB / 16;         // 16-byte chunks per row
     constexpr int TB = kPBN * RB;        // tile bytes (K or V)
@@ -330,7 +370,6 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][TB];
 
     const int kvh = (int)blockIdx.x % p.n_head_kv;
-    const int qblk = p.n_qblk - 1 - (int)blockIdx.x / p.n_head_kv;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -338,22 +377,10 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
     const int hh = lane >> 5;
     const int64_t col_bytes = (int64_t)p.n_head_kv * RB;
 
-    const int rho = wave * 32 + n;
-    const int g = rho / QB;
-    const int tq = qblk * QB + rho % QB;
-    const bool row_ok = tq < p.T;
-    const int h = kvh * G + g;
-    const int qp = p.q_pos0 + tq;
-
-    const int first_tok = qblk * QB;
-    int last_tok = first_tok + QB - 1;
-    if (last_tok > p.T - 1) last_tok = p.T - 1;
-    const int kv_hi = p.q_pos0 + last_tok;
-    const int q_lo = p.q_pos0 + first_tok;
-    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
-    const int tile0 = lo / kPBN;
-    const int tile1 = kv_hi / kPBN;
-    const bool block_full = (qblk + 1) * QB <= p.T;
+    const PrefillRows rows = prefill_rows<G>(p, wave, n);
+    const bool row_ok = rows.row_ok;
+    const int tq = rows.tq, h = rows.h;
+    const int kv_hi = rows.kv_hi, lo = rows.lo, tile0 = rows.tile0, tile1 = rows.tile1;
 
     // tile t -> LDS buffer buf; false (workgroup-uniform) for an invalid page
     auto load = [&](int t, int buf) -> bool {
@@ -421,28 +448,9 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
                     s[pb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qf[4 * j + e], s[pb], 0, 0, 0);
             }
         }
-        const bool edge = dead || pos0 < lo || pos0 + kPBN - 1 > q_lo || !block_full;
-        if (edge) {
-#pragma unroll
-            for (int pb = 0; pb < 2; ++pb) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                    s[pb][i] = (!dead && row_ok && kp >= lo && kp <= qp) ? s[pb][i] : -INFINITY;
-                }
-            }
-        }
-        float mt = -INFINITY;
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
-        mt = fmaxf(mt, xor32(mt)) * p.scale_log2;
-        float alpha = 1.0f;
-        if (mt > m_run + kRescaleLog2) {
-            alpha = __builtin_amdgcn_exp2f(m_run - mt);
-            m_run = mt;
-        }
+        const bool edge = prefill_edge(rows, pos0, dead);
+        if (edge) prefill_mask(s, rows, pos0, hh, dead);
+        const float alpha = prefill_rescale(s, p.scale_log2, m_run);
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         float pe[2][16];
         float ls = 0.0f;
@@ -483,18 +491,7 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
         ok_cur = ok_next;
     }
 
-    l_run += xor32(l_run);
-    if (row_ok) {
-        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-        float *orow = p.out + ((int64_t)tq * p.n_head + h) * HD;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                orow[32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i] * inv;
-            }
-        }
-    }
+    prefill_write<HD>(o, l_run, rows, p, hh);
 }
 
 // Q8_0 cache (head_dim 64 or 128), ggml's arithmetic: Q is quantised to Q8_0
@@ -511,7 +508,6 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
     static_assert(HD == 64 || HD == 128, "head_dim");
     constexpr int NB = HD / 32;           // blocks per row
     constexpr int DB = HD / 32;
-    constexpr int QB = 128 / G;
     constexpr int ROW = HD * 2 + 64;      // padded f16 V row (bytes)
     constexpr int QROW = HD;              // int8 K row in LDS (bytes)
     constexpr int SW = QROW / 16 - 1;     // K chunk swizzle mask
@@ -521,7 +517,6 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kPBN * ROW];
 
     const int kvh = (int)blockIdx.x % p.n_head_kv;
-    const int qblk = p.n_qblk - 1 - (int)blockIdx.x / p.n_head_kv;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -529,22 +524,10 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
     const int hh = lane >> 5;
     const int64_t col_bytes = (int64_t)p.n_head_kv * RB;
 
-    const int rho = wave * 32 + n;
-    const int g = rho / QB;
-    const int tq = qblk * QB + rho % QB;
-    const bool row_ok = tq < p.T;
-    const int h = kvh * G + g;
-    const int qp = p.q_pos0 + tq;
-
-    const int first_tok = qblk * QB;
-    int last_tok = first_tok + QB - 1;
-    if (last_tok > p.T - 1) last_tok = p.T - 1;
-    const int kv_hi = p.q_pos0 + last_tok;
-    const int q_lo = p.q_pos0 + first_tok;
-    const int lo = p.kv_lo > 0 ? p.kv_lo : 0;
-    const int tile0 = lo / kPBN;
-    const int tile1 = kv_hi / kPBN;
-    const bool block_full = (qblk + 1) * QB <= p.T;
+    const PrefillRows rows = prefill_rows<G>(p, wave, n);
+    const bool row_ok = rows.row_ok;
+    const int tq = rows.tq, h = rows.h;
+    const int kv_hi = rows.kv_hi, lo = rows.lo, tile0 = rows.tile0, tile1 = rows.tile1;
 
     // staging unit of this thread: position sp_, block sc (threads past
     // kPBN * NB stage nothing)
@@ -707,28 +690,20 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
                 }
             }
         }
-        const bool edge = dead || pos0 < lo || pos0 + kPBN - 1 > q_lo || !block_full;
+        // prefill_edge and prefill_mask spelled out: with the helper calls the
+        // register allocator spills 296 bytes in this kernel at head_dim 128
+        const bool edge = dead || pos0 < lo || pos0 + kPBN - 1 > rows.q_lo || !rows.block_full;
         if (edge) {
 #pragma unroll
             for (int pb = 0; pb < 2; ++pb) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int kp = pos0 + 32 * pb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                    s[pb][i] = (!dead && row_ok && kp >= lo && kp <= qp) ? s[pb][i] : -INFINITY;
+                    s[pb][i] = (!dead && row_ok && kp >= lo && kp <= rows.qp) ? s[pb][i] : -INFINITY;
                 }
             }
         }
-        float mt = -INFINITY;
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
-        mt = fmaxf(mt, xor32(mt)) * p.scale_log2;
-        float alpha = 1.0f;
-        if (mt > m_run + kRescaleLog2) {
-            alpha = __builtin_amdgcn_exp2f(m_run - mt);
-            m_run = mt;
-        }
+        const float alpha = prefill_rescale(s, p.scale_log2, m_run);
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         half8 pbv[2][2];
 #pragma unroll
@@ -776,18 +751,7 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
         __syncthreads();
     }
 
-    l_run += xor32(l_run);
-    if (row_ok) {
-        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-        float *orow = p.out + ((int64_t)tq * p.n_head + h) * HD;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                orow[32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i] * inv;
-            }
-        }
-    }
+    prefill_write<HD>(o, l_run, rows, p, hh);
 }
 
 template <int HD, int G>
