@@ -906,15 +906,19 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave);
     pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
     const PlanRaw raw = plan_load(p, lane);
-    const int hq = n % G;
-    floatx4 qraw[NB][4];
+    // Q of the g heads, one 8-element chunk per thread (one load of each Q
+    // value per workgroup: per-lane copies would queue ahead of the first
+    // tile's K/V requests)
+    static_assert(G * HD / 8 <= 256, "one Q chunk per thread");
+    const bool q_thread = threadIdx.x < G * HD / 8;
+    floatx4 qx0 = floatx4{}, qx1 = floatx4{};
     auto load_q = [&](int bq) {
-        const float *qr = p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G + hq) * HD;
-#pragma unroll
-        for (int c = 0; c < NB; ++c)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                qraw[c][j] = reinterpret_cast<const floatx4 *>(qr + 32 * c + 16 * hh)[j];
+        if (q_thread) {
+            const floatx4 *qr = reinterpret_cast<const floatx4 *>(
+                p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
+            qx0 = qr[2 * threadIdx.x];
+            qx1 = qr[2 * threadIdx.x + 1];
+        }
     };
     load_q(b_g);
     Raw ra, rb;
@@ -939,32 +943,32 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
         load_q(b);
     }
 
-    // Q8_0 of Q, the MFMA A operand: lane row m = n is head n % G, block c,
-    // elements 16hh .. 16hh+15; staged in LDS (read per tile, which keeps 16
-    // registers for the tile pipeline).
+    // Q8_0 of Q, the MFMA A operand (lane row n is head n % G, block c,
+    // elements 16hh .. 16hh+15), staged in LDS and read per tile.  Thread i
+    // holds dims 8k .. 8k+7 (k = i % (HD/8)) of head i / (HD/8), a quarter of
+    // block k / 4; the block's amax is taken over the 4 adjacent lanes.
     {
+        const float x[8] = {qx0[0], qx0[1], qx0[2], qx0[3], qx1[0], qx1[1], qx1[2], qx1[3]};
+        float amax = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NB; ++c) {
-            float x[16];
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
+        amax = fmaxf(amax, dpp_row<0xB1>(amax));  // lane ^ 1
+        amax = fmaxf(amax, dpp_row<0x4E>(amax));  // lane ^ 2
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        int w[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const floatx4 v4 = qraw[c][j];
-                x[4 * j] = v4[0]; x[4 * j + 1] = v4[1]; x[4 * j + 2] = v4[2]; x[4 * j + 3] = v4[3];
-            }
-            float amax = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(x[j]));
-            amax = fmaxf(amax, xor32(amax));
-            const float d = amax / 127.0f;
-            const float id = d != 0.0f ? 1.0f / d : 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int q0 = (int)roundf(x[4 * j] * id), q1 = (int)roundf(x[4 * j + 1] * id);
-                const int q2 = (int)roundf(x[4 * j + 2] * id), q3 = (int)roundf(x[4 * j + 3] * id);
-                const int w4 = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
-                if (wave == 0 && n < G) lds_qa[n][c][hh][j] = w4;
-            }
-            if (wave == 0 && hh == 0 && n < G) lds_dq[n][c] = (float)(_Float16)d;
+        for (int j = 0; j < 2; ++j) {
+            const int q0 = (int)roundf(x[4 * j] * id), q1 = (int)roundf(x[4 * j + 1] * id);
+            const int q2 = (int)roundf(x[4 * j + 2] * id), q3 = (int)roundf(x[4 * j + 3] * id);
+            w[j] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
+        }
+        if (q_thread) {
+            const int hq = (int)threadIdx.x / (HD / 8), k = (int)threadIdx.x % (HD / 8);
+            int *dst = reinterpret_cast<int *>(&lds_qa[hq][k >> 2][(k >> 1) & 1]) + 2 * (k & 1);
+            dst[0] = w[0];
+            dst[1] = w[1];
+            if ((k & 3) == 0) lds_dq[hq][k >> 2] = (float)(_Float16)d;
         }
     }
 
