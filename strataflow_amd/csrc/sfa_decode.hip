@@ -577,7 +577,7 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
 // MFMAs; at 4 bytes per element the kernel stays bound by HBM at long
 // contexts.
 template <int HD, int G>
-__global__ __launch_bounds__(256, 2) void decode_f32_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeParams p) {
     static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
     static_assert(G >= 1 && G <= 32 && (32 % G) == 0, "group size");
     constexpr int KH = HD / 2;           // K floats per lane (half a row)
@@ -1101,8 +1101,9 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
         // halves hold every head, so only half 0 and i < g count
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (G == 8) {
-                if (hh) l_run[4 + i] += pv[i]; else l_run[i] += pv[i];
+            if (G == 8) {  // selects, not l_run[4hh + i]: a per-lane index puts l_run in scratch
+                l_run[i] += hh ? 0.0f : pv[i];
+                l_run[4 + i] += hh ? pv[i] : 0.0f;
             } else if (i < G && hh == 0) {
                 l_run[i] += pv[i];
             }

@@ -171,7 +171,8 @@ def test_decode_q8_golden(gpu, oracle_mod):
     assert_close(out, g["exact"], max_abs=Q8_EXACT_ABS, rel_l2=Q8_EXACT_REL, what="q8 vs exact golden")
 
 
-@pytest.mark.parametrize("shape", [(32, 8, 128), (8, 4, 64), (16, 2, 128), (8, 8, 128), (16, 16, 64)])
+@pytest.mark.parametrize("shape", [(32, 8, 128), (8, 4, 64), (16, 2, 128), (16, 2, 64), (8, 8, 128),
+                                   (16, 16, 64)])
 @pytest.mark.parametrize("n_kv", [1, 33, 257, 1000])
 def test_decode_q8_shapes(gpu, oracle_mod, shape, n_kv):
     Hq, Hkv, hd = shape
