@@ -50,11 +50,13 @@ struct DecodeParams {
     int guess_splits;     // the host's guess of splits per sequence (all at max_seq_len)
     int guess_tiles;      // and of its tiles; the device plan decides
     int one_split;        // 1: no merge pass runs (one sequence, guessed one split)
+    int cols_waves;       // Q8_0: kv heads per column-layout workgroup, 0 = per-kv-head layout
     float scale_log2;     // scale * log2(e)
     float *part;          // [Hkv][split_row][G][HD + 4]: one (o, m, l) record per slot
 };
 
 constexpr int kDecodeWaves = 4;
+constexpr int kColsWaves = 8;    // most waves (kv heads) of a column-layout Q8_0 workgroup
 constexpr int kMaxSplits = 256;  // splits per (sequence, kv head)
 constexpr int kMaxPlanTiles = 1 << 30;  // bound on the tiles of one call (all sequences)
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold: P <= 2^8
@@ -811,38 +813,52 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
 //   - V is dequantised in registers (q * d, rounded to f16) into the same
 //     LDS tile layout as the f16 path, and P goes through LDS to the P^T
 //     operand; PV is the f16 path's O^T = V^T * P^T.
-template <int HD, int G>
-__global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodeParams p) {
+// COLS = false: one workgroup per (kv head, row slot), its four waves take
+// every fourth tile of the split and merge through LDS.  COLS = true (long
+// batches): one workgroup per (row slot, group of up to kColsWaves kv heads),
+// wave w serves kv head group * waves + w over every tile of the split and
+// writes its own record.  The waves of a workgroup then read whole position
+// columns together (the 136-byte rows of neighbouring kv heads share cache
+// lines) and the split epilogue needs no workgroup merge.
+template <int HD, int G, bool COLS>
+__global__ __launch_bounds__(COLS ? 64 * kColsWaves : 256, (COLS || G <= 4) ? 2 : 1)
+void decode_q8_kernel(DecodeParams p) {
     static_assert(HD == 64 || HD == 128, "head_dim");
     static_assert(G >= 1 && G <= 8 && (8 % G) == 0, "group size");
     constexpr int NB = HD / 32;          // blocks per row
     constexpr int DB = HD / 32;          // 32-dim blocks of the PV output
     constexpr int VROW = HD * 2 + 16;    // padded LDS row of the f16 V tile
     constexpr int VBL = NB / 2;          // V blocks dequantised per lane
+    constexpr int NW = COLS ? kColsWaves : kDecodeWaves;  // most waves per workgroup
+    constexpr int QW = COLS ? kColsWaves : 1;             // Q copies (one per kv head)
+    constexpr int MW = COLS ? 1 : kDecodeWaves;           // wave records merged in LDS
+    constexpr int TS = COLS ? 1 : kDecodeWaves;           // tile stride of a wave
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds_v[kDecodeWaves][kTile * VROW];
-    __shared__ __attribute__((aligned(16))) _Float16 lds_p[kDecodeWaves][G][kTile];
-    __shared__ float lds_dq[G][NB];
-    __shared__ intx4 lds_qa[G][NB][2];
-    __shared__ float lds_m[kDecodeWaves][G];
-    __shared__ float lds_l[kDecodeWaves][G];
-    __shared__ float lds_o[kDecodeWaves][G][HD];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[NW][kTile * VROW];
+    __shared__ __attribute__((aligned(16))) _Float16 lds_p[NW][G][kTile];
+    __shared__ float lds_dq[QW][G][NB];
+    __shared__ intx4 lds_qa[QW][G][NB][2];
+    __shared__ float lds_m[MW][G];
+    __shared__ float lds_l[MW][G];
+    __shared__ float lds_o[MW][G][HD];
 
     // slot of kv head kvh's row and the host's guess of its sequence / split
-    const int kvh = (int)blockIdx.x / p.split_row;
-    const int slot = (int)blockIdx.x - kvh * p.split_row;
-    int b_g = slot / p.guess_splits;
-    if (b_g >= p.n_seq) b_g = p.n_seq - 1;
-    const int split_g = slot - b_g * p.guess_splits;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int n = lane & 31;   // tile position (QK) / MFMA column (PV)
     const int hh = lane >> 5;
+    const int grp = (int)blockIdx.x / p.split_row;
+    const int slot = (int)blockIdx.x - grp * p.split_row;
+    const int kvh = COLS ? grp * ((int)blockDim.x >> 6) + wave : grp;
+    const int qw = COLS ? wave : 0;
+    int b_g = slot / p.guess_splits;
+    if (b_g >= p.n_seq) b_g = p.n_seq - 1;
+    const int split_g = slot - b_g * p.guess_splits;
     const int32_t *pt = p.page_table + (int64_t)b_g * p.max_pages;
     const int Hkv = p.n_head_kv;
     const int64_t col_bytes = (int64_t)Hkv * p.row_bytes;
     uint8_t *vt = lds_v[wave];
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int wave_u = __builtin_amdgcn_readfirstlane(COLS ? 0 : wave);
 
     // K operand of block c for lane (row n, half hh): quants 16hh..16hh+15 of
     // block c and the block scale; V: blocks VBL*hh .. of row n.  All kept
@@ -903,21 +919,24 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     // and the lane's Q values are issued before the first tile's K/V burst.
     int t_guess, t_guess_hi;
     split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
-    t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave);
+    t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave_u);
     pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
     const PlanRaw raw = plan_load(p, lane);
-    // Q of the g heads, one 8-element chunk per thread (one load of each Q
-    // value per workgroup: per-lane copies would queue ahead of the first
-    // tile's K/V requests)
+    // Q of the g heads of a kv head, one 8-element chunk per thread (one load
+    // of each Q value per workgroup: per-lane copies would queue ahead of the
+    // first tile's K/V requests); COLS: each wave its own kv head's chunks
     static_assert(G * HD / 8 <= 256, "one Q chunk per thread");
-    const bool q_thread = threadIdx.x < G * HD / 8;
-    floatx4 qx0 = floatx4{}, qx1 = floatx4{};
+    constexpr int QCH = COLS ? (G * HD / 8 + 63) / 64 : 1;  // chunks per thread
+    const int q_idx0 = COLS ? lane : (int)threadIdx.x;
+    floatx4 qx0[QCH], qx1[QCH];
     auto load_q = [&](int bq) {
-        if (q_thread) {
-            const floatx4 *qr = reinterpret_cast<const floatx4 *>(
-                p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
-            qx0 = qr[2 * threadIdx.x];
-            qx1 = qr[2 * threadIdx.x + 1];
+        const floatx4 *qr = reinterpret_cast<const floatx4 *>(
+            p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
+#pragma unroll
+        for (int k = 0; k < QCH; ++k) {
+            const int idx = q_idx0 + 64 * k;
+            qx0[k] = idx < G * HD / 8 ? qr[2 * idx] : floatx4{};
+            qx1[k] = idx < G * HD / 8 ? qr[2 * idx + 1] : floatx4{};
         }
     };
     load_q(b_g);
@@ -930,7 +949,8 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
         // without tiles, or, for one sequence, the slot that would own it
         if (p.n_seq == 1 && slot == 0 && sp.n_b == 0) {
             float *out0 = p.out + (int64_t)kvh * G * HD;
-            for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out0[i] = 0.0f;
+            for (int i = COLS ? lane : (int)threadIdx.x; i < G * HD; i += COLS ? 64 : (int)blockDim.x)
+                out0[i] = 0.0f;
         }
         return;
     }
@@ -944,11 +964,13 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     }
 
     // Q8_0 of Q, the MFMA A operand (lane row n is head n % G, block c,
-    // elements 16hh .. 16hh+15), staged in LDS and read per tile.  Thread i
+    // elements 16hh .. 16hh+15), staged in LDS and read per tile.  Chunk i
     // holds dims 8k .. 8k+7 (k = i % (HD/8)) of head i / (HD/8), a quarter of
     // block k / 4; the block's amax is taken over the 4 adjacent lanes.
-    {
-        const float x[8] = {qx0[0], qx0[1], qx0[2], qx0[3], qx1[0], qx1[1], qx1[2], qx1[3]};
+#pragma unroll
+    for (int kq = 0; kq < QCH; ++kq) {
+        const floatx4 qa0 = qx0[kq], qa1 = qx1[kq];
+        const float x[8] = {qa0[0], qa0[1], qa0[2], qa0[3], qa1[0], qa1[1], qa1[2], qa1[3]};
         float amax = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
@@ -963,12 +985,13 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
             const int q2 = (int)roundf(x[4 * j + 2] * id), q3 = (int)roundf(x[4 * j + 3] * id);
             w[j] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
         }
-        if (q_thread) {
-            const int hq = (int)threadIdx.x / (HD / 8), k = (int)threadIdx.x % (HD / 8);
-            int *dst = reinterpret_cast<int *>(&lds_qa[hq][k >> 2][(k >> 1) & 1]) + 2 * (k & 1);
+        const int idx = q_idx0 + 64 * kq;
+        if (idx < G * HD / 8) {
+            const int hq = idx / (HD / 8), k = idx % (HD / 8);
+            int *dst = reinterpret_cast<int *>(&lds_qa[qw][hq][k >> 2][(k >> 1) & 1]) + 2 * (k & 1);
             dst[0] = w[0];
             dst[1] = w[1];
-            if ((k & 3) == 0) lds_dq[hq][k >> 2] = (float)(_Float16)d;
+            if ((k & 3) == 0) lds_dq[qw][hq][k >> 2] = (float)(_Float16)d;
         }
     }
 
@@ -1007,11 +1030,11 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
                 kq[2] = (int)__builtin_amdgcn_alignbyte(x[3], x[2], 2);
                 kq[3] = (int)__builtin_amdgcn_alignbyte(r.kx[c / 2], x[3], 2);
             }
-            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lds_qa[n % G][c][hh], kq, intx16{}, 0, 0, 0);
+            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lds_qa[qw][n % G][c][hh], kq, intx16{}, 0, 0, 0);
             const uint32_t dbits = (c & 1) ? (r.kd[c] >> 16) : (r.kd[c] & 0xffffu);
             const float dk = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sv[i] += (float)acc[i] * (dk * lds_dq[(4 * hh + i) % G][c]);
+            for (int i = 0; i < 4; ++i) sv[i] += (float)acc[i] * (dk * lds_dq[qw][(4 * hh + i) % G][c]);
             // one block's 16-register accumulator live at a time
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1160,14 +1183,14 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
     // into the other set as soon as a tile's raw registers are consumed, so
     // one tile is in flight while the current one finishes
     float sv[4];
-    for (; t < tile_hi; t += 2 * kDecodeWaves) {
-        const int t1 = t + kDecodeWaves;
+    for (; t < tile_hi; t += 2 * TS) {
+        const int t1 = t + TS;
         if (ok_a) consume1(t, ra, sv);
         const bool ok_b = t1 < tile_hi ? issue(t1, rb) : false;
         if (ok_a) consume2(t, sv);
         if (t1 >= tile_hi) break;
         if (ok_b) consume1(t1, rb, sv);
-        ok_a = t1 + kDecodeWaves < tile_hi ? issue(t1 + kDecodeWaves, ra) : false;
+        ok_a = t1 + TS < tile_hi ? issue(t1 + TS, ra) : false;
         if (ok_b) consume2(t1, sv);
     }
 
@@ -1184,8 +1207,29 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_q8_kernel(DecodePa
 #pragma unroll
     for (int h = 1; h < G; ++h)
         if (n % G == h) { m_col = m_run[h]; l_col = Lh[h]; }
-    split_epilogue<HD, G>(o, m_col, l_col, lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b,
-                          wave, n, hh);
+    if constexpr (COLS) {
+        // this wave's record: column n < g holds head n
+        if (n < G) {
+            const float inv = l_col > 0.0f ? 1.0f / l_col : 0.0f;
+            float *part = p.part + ((int64_t)kvh * p.split_row + sp.rec0 + sp.split) * G * (HD + 4) + n * (HD + 4);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int dim = 32 * d + 8 * (i >> 2) + 4 * hh + (i & 3);
+                    if (sp.n_b == 1) out_b[n * HD + dim] = o[d][i] * inv;
+                    else part[dim] = o[d][i];
+                }
+            }
+            if (sp.n_b != 1 && hh == 0) {
+                part[HD] = m_col;
+                part[HD + 1] = l_col;
+            }
+        }
+    } else {
+        split_epilogue<HD, G>(o, m_col, l_col, lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b,
+                              wave, n, hh);
+    }
 }
 
 // Second pass: out = sum_s o_s * 2^(m_s - M) / sum_s l_s * 2^(m_s - M) over
@@ -1291,17 +1335,18 @@ struct SplitPlan {
     int guess_tiles;
 };
 
-// About 512 workgroups (two 4-wave workgroups per CU at these register
-// footprints, over 256 CUs): the row of each kv head gets 512 / Hkv slots, at
+// About 2048 waves (two per SIMD at these register footprints, over 256 CUs):
+// the row of each kv head gets 2048 / (Hkv * waves per slot) slots (512 four-
+// wave workgroups; with the column layout one wave per (slot, kv head)), at
 // most kMaxSplits, no more than the batch could use (every sequence's widest
 // span of max_seq_len positions, which covers one tile more when a window start
 // is not tile-aligned, cut into kDecodeWaves-tile splits), at least B, rounded
 // up to a multiple of 8.  The device plan deals the slots out by length.
-SplitPlan plan_splits(int B, int Hkv, int max_seq_len, bool windowed) {
-    const int wg_target = 512;
+SplitPlan plan_splits(int B, int Hkv, int max_seq_len, bool windowed, bool cols) {
+    const int slot_target = 2048 / (cols ? 1 : kDecodeWaves);
     const int tiles = ceil_div(max_seq_len, kTile);
     const int span_tiles = windowed ? ceil_div(max_seq_len - 1, kTile) + 1 : tiles;
-    int row = (wg_target + Hkv - 1) / Hkv;
+    int row = (slot_target + Hkv - 1) / Hkv;
     if (row > kMaxSplits) row = kMaxSplits;
     const long long most = (long long)B * ceil_div(span_tiles, kDecodeWaves);
     if (row > most) row = (int)most;
@@ -1313,9 +1358,39 @@ SplitPlan plan_splits(int B, int Hkv, int max_seq_len, bool windowed) {
     return SplitPlan{row, g > 0 ? g : 1, tiles};
 }
 
+// The column layout of the Q8_0 kernel (g <= 4) serves batches of two or more
+// sequences with at least kColsMinTiles tiles in all (B times the widest span).
+// One sequence keeps the per-kv-head layout: its merge pass then reads 4x the
+// records over only Hkv * g workgroups (B = 1 at 32k: 27.6 -> 33.2 us per
+// layer with the column layout, B = 8 over 8k..32k: 107.6 -> 103.6 us).
+constexpr long long kColsMinTiles = 1024;
+bool use_cols(int kv_type, int HD, int G, int B, int max_seq_len, bool windowed) {
+    if (kv_type != SFA_KV_Q8_0 || HD < 64 || G > 4 || B < 2) return false;
+    const int tiles = ceil_div(max_seq_len, kTile);
+    const int span_tiles = windowed ? ceil_div(max_seq_len - 1, kTile) + 1 : tiles;
+    return (long long)B * span_tiles >= kColsMinTiles;
+}
+
+// kv heads per column-layout workgroup: the largest of 8, 4, 2, 1 dividing Hkv
+int cols_waves_of(int Hkv) {
+    for (int w = kColsWaves; w > 1; w /= 2)
+        if (Hkv % w == 0) return w;
+    return 1;
+}
+
 size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
-    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, true);  // the larger row
-    return (size_t)Hkv * sp.split_row * G * (HD + 4) * sizeof(float);
+    // the larger row of both layouts, windowed (one tile more)
+    const SplitPlan a = plan_splits(B, Hkv, max_seq_len, true, false);
+    const SplitPlan c = plan_splits(B, Hkv, max_seq_len, true, true);
+    const int row = a.split_row > c.split_row ? a.split_row : c.split_row;
+    return (size_t)Hkv * row * G * (HD + 4) * sizeof(float);
+}
+
+template <int HD, int G>
+static void launch_merge(const DecodeParams &p, int B, int Hkv, int passes, hipStream_t s) {
+    if ((passes & 2) && !p.one_split)
+        hipLaunchKernelGGL((decode_merge_kernel<HD, G>), dim3(B * Hkv * G), dim3(kMergeThreads<HD>), 0,
+                           s, p);
 }
 
 // pass bit 1: split-K pass, bit 2: merge pass
@@ -1324,17 +1399,22 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
     if (passes & 1) {
         dim3 grid(p.split_row * Hkv);
         if (p.kv_type == SFA_KV_Q8_0) {
+            if constexpr (HD >= 64 && G <= 4) {
+                if (p.cols_waves > 0) {
+                    hipLaunchKernelGGL((decode_q8_kernel<HD, G, true>), dim3(p.split_row * (Hkv / p.cols_waves)),
+                                       dim3(64 * p.cols_waves), 0, s, p);
+                    return launch_merge<HD, G>(p, B, Hkv, passes, s);
+                }
+            }
             if constexpr (HD >= 64 && G <= 8)
-                hipLaunchKernelGGL((decode_q8_kernel<HD, G>), grid, dim3(256), 0, s, p);
+                hipLaunchKernelGGL((decode_q8_kernel<HD, G, false>), grid, dim3(256), 0, s, p);
         } else if (p.kv_type == SFA_KV_F32) {
             hipLaunchKernelGGL((decode_f32_kernel<HD, G>), grid, dim3(256), 0, s, p);
         } else {
             hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
         }
     }
-    if ((passes & 2) && !p.one_split)
-        hipLaunchKernelGGL((decode_merge_kernel<HD, G>), dim3(B * Hkv * G), dim3(kMergeThreads<HD>), 0,
-                           s, p);
+    launch_merge<HD, G>(p, B, Hkv, passes, s);
 }
 
 template <int HD>
@@ -1362,7 +1442,8 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
         return SFA_ERR_INVALID_ARGUMENT;
     const size_t need = decode_workspace_bytes(B, Hkv, G, HD, max_seq_len);
     if (workspace == nullptr || ws_bytes < need) return SFA_ERR_INVALID_ARGUMENT;
-    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, kv_lo != nullptr);
+    const bool cols = use_cols(kv->kv_type, HD, G, B, max_seq_len, kv_lo != nullptr);
+    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, kv_lo != nullptr, cols);
 
     DecodeParams p;
     p.k_pages = static_cast<const uint8_t *>(kv->k_pages);
@@ -1387,6 +1468,7 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     p.guess_splits = sp.guess_splits;
     p.guess_tiles = sp.guess_tiles;
     p.one_split = B == 1 && sp.guess_splits == 1;
+    p.cols_waves = cols ? cols_waves_of(Hkv) : 0;
     p.scale_log2 = scale * 1.4426950408889634f;
     p.part = static_cast<float *>(workspace);
 

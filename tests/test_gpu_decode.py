@@ -239,6 +239,22 @@ def test_decode_split_plan_batches(gpu, oracle_mod, kv_type, B):
     assert np.all(out[0] == 0)
 
 
+@pytest.mark.parametrize("shape", [(8, 8, 128), (8, 4, 64), (12, 6, 64), (4, 1, 128)])
+def test_decode_q8_column_layout(gpu, oracle_mod, shape):
+    # a batch with >= 1024 tiles in all takes the Q8_0 column layout (one wave
+    # per kv head, workgroups of 8, 4, 2 or 1 kv heads for these shapes)
+    Hq, Hkv, hd = shape
+    B = 40
+    rng = np.random.default_rng(300 + Hkv)
+    seq = rng.integers(1, 900, B)
+    seq[3] = 899
+    seq[5] = 0
+    c = Case(oracle_mod, seq_lens=seq, n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=8, seed=310 + Hkv)
+    out = c.decode(max_seq_len=900)
+    assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 column layout {shape} vs ggml")
+    assert np.all(out[5] == 0)
+
+
 def test_decode_span_beyond_max_seq_len(gpu, oracle_mod):
     # a span longer than max_seq_len is attended in full by longer splits
     c = Case(oracle_mod, seq_lens=[3000, 200], seed=210)
