@@ -192,7 +192,10 @@ def decode_leg(torch, key, lens, kv_type, steps, warmup, seed):
     alg = 2 * sum(lens) * HKV * row + len(lens) * HQ * HD * 4 * 2
     us_layer = ms * 1e3 / N_LAYER
     ach = alg / (k_mean * 1e-6) / 1e9
-    kname = {0: "decode_f32_kernel<128,4>", 1: "decode_f16_kernel<128,4>", 8: "decode_q8_kernel<128,4>"}[kv_type]
+    # Q8_0 batches of two or more with >= 1024 tiles in all run the column layout
+    cols = kv_type == 8 and len(lens) >= 2 and len(lens) * ((mx + 31) // 32) >= 1024
+    kname = {0: "decode_f32_kernel<128,4>", 1: "decode_f16_kernel<128,4>",
+             8: f"decode_q8_kernel<128,4,{'true' if cols else 'false'}>"}[kv_type]
     res = {
         "workload": f"decode-attn {KV_NAMES[kv_type]} KV, Mixtral GQA 32q/8kv hd128, "
                     f"B={len(lens)}, context {lens if len(lens) > 1 else lens[0]}, 256-token pages "
