@@ -97,3 +97,7 @@ def test_decode_workspace_bytes():
     assert n1 > 0 and n8 >= n1
     assert lib.sfa_decode_workspace_bytes(ctypes.byref(d), 0, 4096) == 0
     assert lib.sfa_decode_workspace_bytes(ctypes.byref(desc(head_dim=96)), 1, 4096) == 0
+    # a long Q8_0 batch runs the column layout: 2048 / Hkv = 256 split records
+    # per kv head, each g * (head_dim + 4) floats
+    q8 = desc(kv_type=_lib.SFA_KV_Q8_0)
+    assert lib.sfa_decode_workspace_bytes(ctypes.byref(q8), 8, 32768) >= 8 * 256 * 4 * (128 + 4) * 4
