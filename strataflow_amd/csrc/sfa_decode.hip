@@ -818,8 +818,12 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
 // batches): one workgroup per (row slot, group of up to kColsWaves kv heads),
 // wave w serves kv head group * waves + w over every tile of the split and
 // writes its own record.  The waves of a workgroup then read whole position
-// columns together (the 136-byte rows of neighbouring kv heads share cache
-// lines) and the split epilogue needs no workgroup merge.
+// columns together and the split epilogue needs no workgroup merge.  The
+// 136-byte rows of neighbouring kv heads share cache lines, fetched once only
+// while the sharers stay close in time: over a long split unsynchronised waves
+// drift apart, so a barrier every other loop trip (four tiles) keeps them in
+// step (B = 8 over 8k..32k: 452 -> 392 MiB read per layer; a barrier every
+// trip reads 377 MiB but waits longer than it saves).
 template <int HD, int G, bool COLS>
 __global__ __launch_bounds__(COLS ? 64 * kColsWaves : 256, (COLS || G <= 4) ? 2 : 1)
 void decode_q8_kernel(DecodeParams p) {
@@ -1183,6 +1187,7 @@ void decode_q8_kernel(DecodeParams p) {
     // into the other set as soon as a tile's raw registers are consumed, so
     // one tile is in flight while the current one finishes
     float sv[4];
+    int trip = 0;
     for (; t < tile_hi; t += 2 * TS) {
         const int t1 = t + TS;
         if (ok_a) consume1(t, ra, sv);
@@ -1192,6 +1197,11 @@ void decode_q8_kernel(DecodeParams p) {
         if (ok_b) consume1(t1, rb, sv);
         ok_a = t1 + TS < tile_hi ? issue(t1 + TS, ra) : false;
         if (ok_b) consume2(t1, sv);
+        // column layout: every wave has the same tiles; keep them in step so
+        // the cache lines that neighbouring kv heads share are fetched once
+        if constexpr (COLS) {
+            if ((++trip & 1) == 0) __syncthreads();
+        }
     }
 
     // per-head sums over all 64 lanes (each position counted once per head)
