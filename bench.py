@@ -556,8 +556,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(decode would shard by kv head with no exchange; see DESIGN.md)", file=sys.stderr)
+        print("bench.py measures one GPU only: there is no multi-GPU path "
+              "(decode would shard by kv head, with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import torch
