@@ -333,6 +333,9 @@ int orc_attention(const orc_paged_kv *kv, const float *q, float *out, int32_t n_
         const int nb = hd / QK8_0;
         if (kv->kv_type == ORC_KV_Q8_0)
             kq8 = (orc_block_q8_0 *)malloc(sizeof(orc_block_q8_0) * (size_t)n * Hkv * nb);
+        /* the copies run on all threads, as ggml's cpy / cont ops do */
+        int missing = 0;
+#pragma omp parallel for schedule(static) reduction(|| : missing)
         for (int64_t j = 0; j < n; ++j) {
             for (int kvh = 0; kvh < Hkv; ++kvh) {
                 const uint8_t *kr = orc_row_ptr(kv, 0, pt, max_pages, lo + j, kvh);
@@ -340,7 +343,7 @@ int orc_attention(const orc_paged_kv *kv, const float *q, float *out, int32_t n_
                 float *kd = kh + (j * Hkv + kvh) * hd;
                 float *vd = vh + (j * Hkv + kvh) * hd;
                 if (kr == NULL || vr == NULL) {
-                    rc = 1;
+                    missing = 1;
                     memset(kd, 0, sizeof(float) * hd);
                     memset(vd, 0, sizeof(float) * hd);
                     continue;
@@ -350,6 +353,7 @@ int orc_attention(const orc_paged_kv *kv, const float *q, float *out, int32_t n_
                 if (kq8) memcpy(kq8 + (j * Hkv + kvh) * nb, kr, sizeof(orc_block_q8_0) * nb);
             }
         }
+        if (missing) rc = 1;
         if (rc) {
             free(kh); free(vh); free(kq8);
             return rc;
@@ -397,16 +401,19 @@ int orc_attention(const orc_paged_kv *kv, const float *q, float *out, int32_t n_
             float *kp = (float *)malloc(sizeof(float) * (size_t)n * Hkv * hd);
             float *vt = (float *)malloc(sizeof(float) * (size_t)n * Hkv * hd);
             orc_block_q8_0 *kp8 = NULL;
+#pragma omp parallel for collapse(2) schedule(static)
             for (int kvh = 0; kvh < Hkv; ++kvh)
                 for (int64_t j = 0; j < n; ++j)
                     memcpy(kp + ((int64_t)kvh * n + j) * hd, kh + (j * Hkv + kvh) * hd, sizeof(float) * hd);
             if (kq8) {
                 kp8 = (orc_block_q8_0 *)malloc(sizeof(orc_block_q8_0) * (size_t)n * Hkv * nb);
+#pragma omp parallel for collapse(2) schedule(static)
                 for (int kvh = 0; kvh < Hkv; ++kvh)
                     for (int64_t j = 0; j < n; ++j)
                         memcpy(kp8 + ((int64_t)kvh * n + j) * nb, kq8 + (j * Hkv + kvh) * nb,
                                sizeof(orc_block_q8_0) * nb);
             }
+#pragma omp parallel for collapse(2) schedule(static)
             for (int kvh = 0; kvh < Hkv; ++kvh)
                 for (int d = 0; d < hd; ++d)
                     for (int64_t j = 0; j < n; ++j)
