@@ -276,6 +276,10 @@ __device__ inline bool plan(const DecodeParams &p, const PlanRaw &raw, int j, in
 // written to the workspace, or straight to the output when the sequence has
 // one split.  `l_run` is the lane's full sum over its tiles.
 template <int HD, int G>
+__device__ inline void split_merge(float (*lds_m)[G], float (*lds_l)[G], float (*lds_o)[G][HD],
+                                   const DecodeParams &p, int kvh, int slot, int n_b, float *out_b);
+
+template <int HD, int G>
 __device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run, float l_run,
                                       float (*lds_m)[G], float (*lds_l)[G], float (*lds_o)[G][HD],
                                       const DecodeParams &p, int kvh, int slot, int n_b,
@@ -295,6 +299,14 @@ __device__ inline void split_epilogue(const floatx16 (&o)[HD / 32], float m_run,
         }
     }
     __syncthreads();
+    split_merge<HD, G>(lds_m, lds_l, lds_o, p, kvh, slot, n_b, out_b);
+}
+
+// The four waves' staged (m, l, o) -> the split's record, or the output when
+// the sequence has one split.
+template <int HD, int G>
+__device__ inline void split_merge(float (*lds_m)[G], float (*lds_l)[G], float (*lds_o)[G][HD],
+                                   const DecodeParams &p, int kvh, int slot, int n_b, float *out_b) {
     float *part = p.part + ((int64_t)kvh * p.split_row + slot) * G * (HD + 4);
     for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
         const int g = idx / HD, d = idx % HD;
@@ -569,22 +581,28 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
 
 // F32 decode: the reference's own cache type.  ggml's F32 path keeps Q, K,
 // P and V in f32 (the vec_dot_type of F32 is F32), so both products run on
-// v_mfma_f32_32x32x2_f32 with the f16 kernel's layouts: lane (n, hh) holds
-// half a K row (dims HD/2*hh ..) as the A operand, Q^T column n (head n % g)
-// comes from LDS, S^T lands as in the f16 kernel, and P^T step s of the PV
-// product is exactly the lane's score register s (positions 8(s/4) + 4hh +
-// s%4), so P never moves.  V tiles go straight from the page into the wave's
-// LDS region (global_load_lds, 1 KB per instruction, no registers); V^T
-// operands are 4-byte LDS reads.  Per 32-position tile a wave issues 128
-// MFMAs; at 4 bytes per element the kernel stays bound by HBM at long
-// contexts.
+// v_mfma_f32_16x16x4_f32: 16 columns hold the g heads of the kv head (4x
+// replication at g = 4, against 8x on the 32-column f32 MFMA, which halves the
+// MFMA work).  Lane l serves column c = l % 16 (head c % g) and quarter
+// q = l / 16.  S^T = K * Q^T per 16-position row block rb: quarter q brings
+// dims q*HD/4 .. of K row 16rb + c (contiguous 16-byte loads) and of Q, so
+// the k order of the product is a permutation of the dims; S^T lands with
+// register r of block rb at position 16rb + 4q + r.  O^T += V^T * P^T takes
+// step (rb, r) with quarter q supplying position 16rb + 4q + r, so its P^T
+// operand is the lane's own score register: P never moves.  V tiles go
+// straight from the page into the wave's LDS region (global_load_lds, 1 KB
+// per instruction, no registers) with the 16-byte chunks of row r XORed by
+// 4 * ((r / 4) % 4), so the four quarters' V^T reads (rows 4 apart) fall in
+// different LDS banks.  At 4 bytes per element the kernel stays bound by HBM
+// at long contexts.
 template <int HD, int G>
 __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeParams p) {
     static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
-    static_assert(G >= 1 && G <= 32 && (32 % G) == 0, "group size");
-    constexpr int KH = HD / 2;           // K floats per lane (half a row)
-    constexpr int KV4 = KH / 4;          // 16-byte K loads per lane
-    constexpr int DB = HD / 32;          // 32-dim blocks of the PV output
+    static_assert(G >= 1 && G <= 16 && (16 % G) == 0, "group size");
+    constexpr int QD = HD / 4;           // dims per quarter (k steps per row block)
+    constexpr int KQ4 = QD / 4;          // 16-byte K loads per lane and row block
+    constexpr int KV4 = 2 * KQ4;         // K load instructions per tile
+    constexpr int DB = HD / 16;          // 16-dim blocks of the PV output
     constexpr int VRB = HD * 4;          // V row bytes in LDS (unpadded)
     constexpr int CPR = VRB / 16;        // 16-byte chunks per V row
     constexpr int RPI = kWave / CPR;     // V rows per global_load_lds instruction
@@ -604,8 +622,8 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     const int split_g = slot - b_g * p.guess_splits;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int n = lane & 31;
-    const int hh = lane >> 5;
+    const int c16 = lane & 15;  // MFMA column (head c16 % g) / A-operand row
+    const int qt = lane >> 4;   // quarter: k slot of the MFMA operands
     const int32_t *pt = p.page_table + (int64_t)b_g * p.max_pages;
 
     const int Hkv = p.n_head_kv;
@@ -613,11 +631,12 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     uint8_t *vt = lds_v[wave];
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-    // K of tile t into registers (row n, dims KH*hh ..), V of tile t into the
-    // wave's LDS tile (instruction i: rows i*RPI + lane/CPR, chunk lane%CPR,
-    // lane l at byte 16 l of the instruction's 1 KB run).  Both return false
+    // K of tile t into registers (rows 16rb + c16, dims QD*qt ..), V of tile
+    // t into the wave's LDS tile (instruction i: row r = i*RPI + lane/CPR,
+    // LDS chunk lane%CPR holding the row's chunk (lane%CPR) ^ vswz(r), lane l
+    // at byte 16 l of the instruction's 1 KB run).  Both return false
     // (wave-uniform) for an invalid page id and then load nothing.
-    floatx4 kf[KV4];
+    floatx4 kf[2][KQ4];
     PageWindow pages;
     const uint8_t *vsrc_next = nullptr;
     auto issue_k = [&](int t) -> bool {
@@ -630,9 +649,12 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
         const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
         if (kb == nullptr || vb == nullptr) return false;
         const int64_t off0 = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
-        const uint8_t *kr = kb + off0 + (int64_t)n * col_bytes + KH * 4 * hh;
 #pragma unroll
-        for (int j = 0; j < KV4; ++j) kf[j] = *reinterpret_cast<const floatx4 *>(kr + 16 * j);
+        for (int rb = 0; rb < 2; ++rb) {
+            const uint8_t *kr = kb + off0 + (int64_t)(16 * rb + c16) * col_bytes + QD * 4 * qt;
+#pragma unroll
+            for (int j = 0; j < KQ4; ++j) kf[rb][j] = *reinterpret_cast<const floatx4 *>(kr + 16 * j);
+        }
         vsrc_next = vb + off0;
         return true;
     };
@@ -642,7 +664,7 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
 #pragma unroll
         for (int i = 0; i < VIT; ++i) {
             const int r = i * RPI + lane / CPR;
-            __builtin_amdgcn_global_load_lds(vsrc_next + (int64_t)r * col_bytes + 16 * (lane % CPR),
+            __builtin_amdgcn_global_load_lds(vsrc_next + (int64_t)r * col_bytes + 16 * ((lane % CPR) ^ ((4 * ((r >> 2) & 3)) & (CPR - 1))),
                                              (lds_void *)(vt + 1024 * i), 16, 0, 0);
         }
     };
@@ -706,13 +728,11 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
         issue_v();
     }
     __syncthreads();
-    const float *qcol = lds_q + (n % G) * HD + KH * hh;
-    // V^T operand of step s, dim block d: row 8(s/4) + 4hh + s%4, dim 32d + n
-    const uint8_t *vrow = vt + (4 * hh) * VRB + 4 * n;
+    const float *qcol = lds_q + (c16 % G) * HD + QD * qt;
 
-    floatx16 o[DB];
+    floatx4 o[DB];
 #pragma unroll
-    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    for (int d = 0; d < DB; ++d) o[d] = floatx4{};
     float m_run = -INFINITY;
     float l_run = 0.0f;
 
@@ -720,34 +740,38 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     for (; t < tile_hi; t += kDecodeWaves) {
         const int pos0 = t * kTile;
         const bool dead = !tile_ok;
-        // S^T = K * Q^T, two accumulation chains
-        floatx16 s0 = floatx16{}, s1 = floatx16{};
+        // S^T = K * Q^T: row block rb, k step 4j + e is dim QD*qt + 4j + e
+        floatx4 s[2] = {floatx4{}, floatx4{}};
 #pragma unroll
-        for (int j = 0; j < KV4; ++j) {
+        for (int j = 0; j < KQ4; ++j) {
             const floatx4 qv = *reinterpret_cast<const floatx4 *>(qcol + 4 * j);
-            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][0], qv[0], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][1], qv[1], s1, 0, 0, 0);
-            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][2], qv[2], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][3], qv[3], s1, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+                    s[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[rb][j][e], qv[e], s[rb], 0, 0, 0);
+            }
         }
-        s0 += s1;
         // registers are free: fetch the next tile's K (its V follows the P*V)
         const bool next_ok = t + kDecodeWaves < tile_hi ? issue_k(t + kDecodeWaves) : false;
 
+        // score register 4rb + r is position 16rb + 4qt + r of column c16
         const bool interior = !dead && pos0 >= lo && pos0 + kTile <= n_kv;
-        float sv[16];
+        float sv[8];
         float mt = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float v = s0[i] * p.scale_log2;
+        for (int i = 0; i < 8; ++i) {
+            float v = s[i >> 2][i & 3] * p.scale_log2;
             if (!interior) {
-                const int pp = pos0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                const int pp = pos0 + 16 * (i >> 2) + 4 * qt + (i & 3);
                 v = (!dead && pp >= lo && pp < n_kv) ? v : -INFINITY;
             }
             sv[i] = v;
             mt = fmaxf(mt, v);
         }
         if (__any(mt > m_run + kRescaleLog2)) {
+            // the column's max over the four quarters (lanes c16 + 16q)
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
             mt = fmaxf(mt, xor32(mt));
             const float m_new = fmaxf(m_run, mt);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -760,30 +784,33 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
         }
         first = false;
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        float pe[16];
+        float pe[8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < 8; ++i) {
             pe[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
             l_run += pe[i];
         }
 
         // this tile's V has landed in vt (the next tile's K loads, issued after
         // it, may still fly: loads complete in order); then O^T += V^T * P^T,
-        // rows outside [lo, n_kv) read as 0
-        // (a page's unused tail may hold any bytes)
+        // rows outside [lo, n_kv) read as 0 (a page's unused tail may hold any
+        // bytes).  Step (rb, r): quarter qt supplies row 16rb + 4qt + r, dim
+        // 16d + c16 of the A operand and its own score register as B.
         if (next_ok)
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KV4) : "memory");
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int sidx = 0; sidx < 16; ++sidx) {
-            const int r = 8 * (sidx >> 2) + (sidx & 3);  // + 4hh through vrow
-            const bool row_ok = interior || (!dead && pos0 + r + 4 * hh >= lo && pos0 + r + 4 * hh < n_kv);
+        for (int i = 0; i < 8; ++i) {
+            const int r = 16 * (i >> 2) + 4 * qt + (i & 3);
+            const bool row_ok = interior || (!dead && pos0 + r >= lo && pos0 + r < n_kv);
+            const uint8_t *vrow = vt + r * VRB + 4 * (c16 & 3);
+            const int sw = (4 * ((r >> 2) & 3)) & (CPR - 1);  // the chunk XOR of row r
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
-                float va = *reinterpret_cast<const float *>(vrow + r * VRB + 128 * d);
+                float va = *reinterpret_cast<const float *>(vrow + 16 * ((4 * d + (c16 >> 2)) ^ sw));
                 va = row_ok ? va : 0.0f;
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(va, pe[sidx], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, pe[i], o[d], 0, 0, 0);
             }
         }
         // every V^T read of this tile has returned before the next tile's V
@@ -794,9 +821,24 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     }
     __builtin_amdgcn_s_waitcnt(0);
 
+    // the column's sum over the four quarters; one replica of each head
+    // (columns c16 < g) stages its (m, l, O^T): register r of block d is dim
+    // 16d + 4qt + r
+    l_run += __shfl_xor(l_run, 16, 64);
     l_run += xor32(l_run);
-    split_epilogue<HD, G>(o, m_run, l_run, lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b,
-                          wave, n, hh);
+    if (c16 < G) {
+        if (qt == 0) {
+            lds_m[wave][c16] = m_run;
+            lds_l[wave][c16] = l_run;
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lds_o[wave][c16][16 * d + 4 * qt + r] = o[d][r];
+        }
+    }
+    __syncthreads();
+    split_merge<HD, G>(lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b);
 }
 
 // Q8_0 decode (head_dim 64 or 128).  A row is head_dim/32 ggml block_q8_0
