@@ -175,6 +175,26 @@ SFA_API int sfa_attn_decode_merge(const sfa_kv_desc *kv, const float *q, float *
                                   int32_t B, int32_t max_seq_len, float scale,
                                   void *workspace, size_t ws_bytes, void *stream);
 
+/* Allocation-free decode: sfa_attn_decode without a workspace argument, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference (its attention is one ggml graph whose allocator owns every
+ * buffer).  The split partials live in a library-owned device array of
+ * SFA_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU
+ * until the process ends; its address is looked up once per device.  The call
+ * makes no allocation.  Returns SFA_ERR_OUT_OF_MEMORY when the shape needs
+ * more than SFA_NOALLOC_SCRATCH_BYTES (sfa_decode_workspace_bytes tells the
+ * need).  Every call on one GPU shares that GPU's array: calls that overlap
+ * in time on one GPU (distinct streams, or concurrent host threads) race, so
+ * a caller orders them on one stream.  The passes read only what the same
+ * call wrote, so nothing needs clearing between calls.  Results are bit
+ * identical to sfa_attn_decode's. */
+#define SFA_NOALLOC_SCRATCH_BYTES (8u << 20)
+SFA_API int sfa_attn_decode_noalloc(const sfa_kv_desc *kv, const float *q, float *out,
+                                    const int32_t *page_table, int32_t max_pages,
+                                    const int32_t *seq_len, const int32_t *kv_lo,
+                                    int32_t B, int32_t max_seq_len, float scale, void *stream);
+
 /* Chunked causal prefill of ONE sequence: T query tokens at absolute positions
  * q_pos0 .. q_pos0+T-1, whose K/V are already appended.  Token t attends kv
  * positions kv_lo .. q_pos0+t (causal -INF mask above the diagonal, the

@@ -21,6 +21,9 @@ SFA_KV_F32 = 0
 SFA_KV_F16 = 1
 SFA_KV_Q8_0 = 8
 
+#: scratch bytes of sfa_attn_decode_noalloc (SFA_NOALLOC_SCRATCH_BYTES)
+SFA_NOALLOC_SCRATCH_BYTES = 8 << 20
+
 #: every symbol include/sfa.h declares
 EXPORTS = (
     "sfa_status_str",
@@ -35,6 +38,7 @@ EXPORTS = (
     "sfa_attn_decode",
     "sfa_attn_decode_split",
     "sfa_attn_decode_merge",
+    "sfa_attn_decode_noalloc",
     "sfa_attn_prefill",
     "sfa_page_table_check",
 )
@@ -106,6 +110,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         f = getattr(lib, name)
         f.argtypes = lib.sfa_attn_decode.argtypes
         f.restype = ctypes.c_int
+    lib.sfa_attn_decode_noalloc.argtypes = [D, P, P, P, i32, P, P, i32, i32, ctypes.c_float, P]
+    lib.sfa_attn_decode_noalloc.restype = ctypes.c_int
     lib.sfa_attn_prefill.argtypes = [D, P, P, P, i32, i32, i32, i32, ctypes.c_float, P]
     lib.sfa_attn_prefill.restype = ctypes.c_int
     lib.sfa_page_table_check.argtypes = [D, P, i32, P, P, i32]

@@ -23,6 +23,9 @@ int rope_append_launch(const sfa_kv_desc *kv, float *q, const float *k, const fl
                        const int32_t *page_table, int32_t max_pages, float freq_base,
                        hipStream_t stream);
 int workspace_init_launch(void *ws, size_t bytes, hipStream_t stream);
+int decode_noalloc_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
+                          int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                          int32_t max_seq_len, float scale, hipStream_t stream);
 }  // namespace sfa
 
 namespace {
@@ -159,6 +162,21 @@ SFA_API int sfa_attn_decode_merge(const sfa_kv_desc *kv, const float *q, float *
                                   size_t ws_bytes, void *stream) {
     return decode_entry(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
                         workspace, ws_bytes, stream, 2);
+}
+
+SFA_API int sfa_attn_decode_noalloc(const sfa_kv_desc *kv, const float *q, float *out,
+                                    const int32_t *page_table, int32_t max_pages,
+                                    const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                                    int32_t max_seq_len, float scale, void *stream) {
+    try {
+        const int rc = check_desc(kv);
+        if (rc != SFA_OK) return rc;
+        if (!(scale > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
+        return sfa::decode_noalloc_launch(kv, q, out, page_table, max_pages, seq_len, kv_lo, B,
+                                          max_seq_len, scale, static_cast<hipStream_t>(stream));
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
 }
 
 SFA_API int sfa_attn_prefill(const sfa_kv_desc *kv, const float *q, float *out,

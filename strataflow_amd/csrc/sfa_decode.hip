@@ -22,6 +22,8 @@
 // The kernel boundary is what makes the partials of all eight XCDs visible to
 // the merge (no device-scope fences inside a kernel: on this part each one
 // writes back a whole XCD L2).
+#include <mutex>
+
 #include "sfa_common.h"
 
 namespace sfa {
@@ -1537,6 +1539,59 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     }
     if (rc != SFA_OK) return rc;
     return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+}
+
+// ---- allocation-free decode ----------------------------------------------------
+// sfa_attn_decode_noalloc runs the same two passes over a library-owned
+// scratch array instead of a caller workspace.  The array is a device global
+// of the code object, so every GPU the library runs on holds its own copy
+// until the process ends; its device address is looked up once per device
+// (with that device current) and cached.  Host code never passes the array's
+// name itself to a kernel: on the host that name is only a stand-in.
+static __device__ __align__(256) uint8_t scratch[SFA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the device that owns `stream`.
+int scratch_address(hipStream_t stream, void **out) {
+    int dev = -1;
+    if (stream != nullptr) {
+        if (hipStreamGetDevice(stream, &dev) != hipSuccess) return SFA_ERR_RUNTIME;
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return SFA_ERR_RUNTIME;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return SFA_ERR_RUNTIME;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess) return SFA_ERR_RUNTIME;
+        if (cur != dev && hipSetDevice(dev) != hipSuccess) return SFA_ERR_RUNTIME;
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess || p == nullptr) return SFA_ERR_RUNTIME;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return SFA_OK;
+}
+}  // namespace
+
+int decode_noalloc_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
+                          int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                          int32_t max_seq_len, float scale, hipStream_t stream) {
+    if (B <= 0 || max_seq_len <= 0) return SFA_ERR_INVALID_ARGUMENT;
+    const int Hkv = kv->n_head_kv, G = kv->n_head / kv->n_head_kv;
+    const size_t need = decode_workspace_bytes(B, Hkv, G, kv->head_dim, max_seq_len);
+    if (need > (size_t)SFA_NOALLOC_SCRATCH_BYTES) return SFA_ERR_OUT_OF_MEMORY;
+    void *ws = nullptr;
+    const int rc = scratch_address(stream, &ws);
+    if (rc != SFA_OK) return rc;
+    return decode_launch(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale, ws,
+                         (size_t)SFA_NOALLOC_SCRATCH_BYTES, 3, stream);
 }
 
 }  // namespace sfa
