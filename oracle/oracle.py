@@ -18,6 +18,8 @@ LIB_PATH = HERE / "liboracle.so"
 
 KV_F32, KV_F16, KV_Q8_0 = 0, 1, 8
 GGML, EXACT = 0, 1
+#: forms of ggml's quantize_row_q8_0 (see orc_set_q8_variant in sfa_oracle.c)
+Q8_SCALAR, Q8_AVX2, Q8_NEON = 0, 1, 2
 
 
 class OrcPagedKv(ctypes.Structure):
@@ -65,6 +67,8 @@ def load() -> ctypes.CDLL:
                                   ctypes.c_float, ctypes.c_int, ctypes.c_int]
     lib.orc_attention.restype = ctypes.c_int
     lib.orc_rope_normal.argtypes = [P, P, i32, i32, i32, ctypes.c_float]
+    lib.orc_set_q8_variant.argtypes = [ctypes.c_int]
+    lib.orc_set_q8_variant.restype = ctypes.c_int
     lib.orc_max_threads.argtypes = []
     lib.orc_max_threads.restype = ctypes.c_int
     _lib = lib
@@ -178,6 +182,24 @@ def rope_normal(x: np.ndarray, pos: np.ndarray, freq_base: float) -> np.ndarray:
     n_tok, n_heads, hd = y.shape
     load().orc_rope_normal(y.ctypes.data, pos.ctypes.data, n_tok, n_heads, hd, float(freq_base))
     return y
+
+
+class q8_variant:
+    """Context manager selecting the form of ggml's quantize_row_q8_0 the
+    oracle runs (Q8_SCALAR, Q8_AVX2 or Q8_NEON) for Q8_0 cache appends and the
+    Q8_0 conversion of Q; restores the scalar form on exit."""
+
+    def __init__(self, variant: int):
+        self.variant = variant
+
+    def __enter__(self):
+        if load().orc_set_q8_variant(int(self.variant)) != 0:
+            raise ValueError(f"unknown Q8_0 quantiser form {self.variant}")
+        return self
+
+    def __exit__(self, *exc):
+        load().orc_set_q8_variant(Q8_SCALAR)
+        return False
 
 
 def max_threads() -> int:

@@ -135,11 +135,33 @@ void orc_f16_to_f32_row(const uint16_t *x, float *y, int64_t n) {
 
 /* ---- Q8_0 ------------------------------------------------------------------ */
 
-/* ggml quantize_row_q8_0 (reference form): per block of 32, d = amax / 127,
- * id = d ? 1/d : 0, q = roundf(x * id), d stored as fp16. */
+/* ggml's quantize_row_q8_0 comes in three forms (ggml, tag b11379; all store
+ * d = amax / 127 as fp16 and q = round(x * id) per block of 32):
+ *   ORC_Q8_SCALAR (0): the portable reference form quantize_row_q8_0_ref:
+ *                      id = d ? 1/d : 0, roundf (ties away from zero);
+ *   ORC_Q8_AVX2   (1): the x86 SIMD form: id = amax ? 127/amax : 0, rounded
+ *                      to nearest even (_mm256_round_ps, _MM_ROUND_NEAREST);
+ *   ORC_Q8_NEON   (2): the Arm SIMD form: id = d ? 1/d : 0, nearest even
+ *                      (vcvtnq_s32_f32).
+ * ggml's CPU backend runs the SIMD form of the host it was built for, both for
+ * a cpy into a Q8_0 cache and for the Q8_0 conversion of src1 in mul_mat.  The
+ * form is process-wide (orc_set_q8_variant); the default is the scalar one,
+ * which is what the GPU append writes. */
+#define ORC_Q8_SCALAR 0
+#define ORC_Q8_AVX2 1
+#define ORC_Q8_NEON 2
+static int orc_q8_variant = ORC_Q8_SCALAR;
+
+int orc_set_q8_variant(int v) {
+    if (v < ORC_Q8_SCALAR || v > ORC_Q8_NEON) return 1;
+    orc_q8_variant = v;
+    return 0;
+}
+
 void orc_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
     orc_block_q8_0 *y = (orc_block_q8_0 *)vy;
     const int64_t nb = k / QK8_0;
+    const int var = orc_q8_variant;
     for (int64_t i = 0; i < nb; ++i) {
         float amax = 0.0f;
         for (int j = 0; j < QK8_0; ++j) {
@@ -147,10 +169,14 @@ void orc_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
             if (v > amax) amax = v;
         }
         const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        float id;
+        if (var == ORC_Q8_AVX2) id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        else id = d != 0.0f ? 1.0f / d : 0.0f;
         y[i].d = orc_f32_to_f16(d);
         for (int j = 0; j < QK8_0; ++j) {
-            y[i].qs[j] = (int8_t)roundf(x[i * QK8_0 + j] * id);
+            const float v = x[i * QK8_0 + j] * id;
+            /* nearbyintf rounds to nearest even in the default rounding mode */
+            y[i].qs[j] = (int8_t)(var == ORC_Q8_SCALAR ? roundf(v) : nearbyintf(v));
         }
     }
 }

@@ -82,6 +82,52 @@ def test_q8_0_roundtrip_bound(oracle_mod):
     assert np.all(np.abs(np.take_along_axis(q, amax_idx[..., None], -1)) == 127)
 
 
+def test_q8_0_simd_forms_round_ties_to_even(oracle_mod):
+    # the same amax-127 block as above under ggml's SIMD quantisers (x86 and
+    # Arm): codes are rounded to nearest even, so the ties go the other way
+    x = np.zeros(32, np.float32)
+    x[:8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -126.4, 3.49]
+    for form in (oracle_mod.Q8_AVX2, oracle_mod.Q8_NEON):
+        with oracle_mod.q8_variant(form):
+            b = oracle_mod.quantize_q8_0(x)
+        assert b[:2].view(np.float16)[0] == np.float16(1.0)
+        assert list(b[2:].view(np.int8)[:8]) == [127, 2, -2, 0, 0, 2, -126, 3], form
+    # and the scalar form is restored on exit
+    assert list(oracle_mod.quantize_q8_0(x)[2:].view(np.int8)[:3]) == [127, 3, -3]
+
+
+def test_q8_0_avx2_form_scales_by_127_over_amax(oracle_mod):
+    # amax 1.4442534: in f32, 127/amax = 87.93471 while 1/(amax/127) = 87.9347,
+    # so x = 0.017058112 lands at 1.5000001 (x86 form: code 2) or 1.4999999
+    # (scalar and Arm forms: code 1)
+    x = np.zeros(32, np.float32)
+    x[0], x[1] = np.float32(1.4442534), np.float32(0.017058112)
+    assert np.float32(127) / x[0] != np.float32(1) / (x[0] / np.float32(127))
+    codes = {}
+    for form in (oracle_mod.Q8_SCALAR, oracle_mod.Q8_AVX2, oracle_mod.Q8_NEON):
+        with oracle_mod.q8_variant(form):
+            codes[form] = oracle_mod.quantize_q8_0(x)[2:].view(np.int8)[:2].tolist()
+    assert codes == {oracle_mod.Q8_SCALAR: [127, 1], oracle_mod.Q8_AVX2: [127, 2],
+                     oracle_mod.Q8_NEON: [127, 1]}
+
+
+def test_q8_0_forms_differ_rarely(oracle_mod):
+    # on N(0,1) data the three forms store the same scale and differ in very
+    # few codes (exact ties and one-ulp differences of id at a half-integer)
+    x = np.random.default_rng(3).standard_normal((4096, 128)).astype(np.float32)
+    out = {}
+    for form in (oracle_mod.Q8_SCALAR, oracle_mod.Q8_AVX2, oracle_mod.Q8_NEON):
+        with oracle_mod.q8_variant(form):
+            out[form] = oracle_mod.quantize_q8_0(x).reshape(-1, 34)
+    base = out[oracle_mod.Q8_SCALAR]
+    for form in (oracle_mod.Q8_AVX2, oracle_mod.Q8_NEON):
+        assert np.array_equal(out[form][:, :2], base[:, :2])
+        diff = np.count_nonzero(out[form][:, 2:] != base[:, 2:])
+        assert diff <= 1e-4 * x.size, (form, diff)
+        dq = np.abs(out[form][:, 2:].view(np.int8).astype(int) - base[:, 2:].view(np.int8).astype(int))
+        assert dq.max() <= 1
+
+
 @pytest.mark.parametrize("name", ["attn_q8_gqa4_decode", "attn_q8_gqa2_prefill"])
 def test_q8_0_matches_golden_bytes(oracle_mod, name):
     g = golden(name)
