@@ -42,7 +42,8 @@ typedef struct sfa_pager_config {
     int32_t n_layer;
     int32_t n_head, n_head_kv, head_dim;
     int32_t kv_type;       /* SFA_KV_F32, SFA_KV_F16 or SFA_KV_Q8_0                  */
-    int32_t page_size;     /* positions per page, a multiple of 32                   */
+    int32_t page_size;     /* positions per page, a multiple of 32 (of 64 for steps  */
+                           /* of more than one token per sequence: the prefill)     */
     int32_t n_seq;         /* sequences decoded together                             */
     int32_t n_ctx;         /* positions per sequence (KvStore capacity)              */
     int32_t window;        /* resident positions per sequence; 0 = n_ctx (no paging) */
@@ -59,6 +60,7 @@ typedef struct sfa_pager_stats {
     int64_t dev_pages_in_use;
     int64_t cold_pages_in_use;
     int64_t bytes_evicted;    /* device-to-host bytes of the eviction copies  */
+    int64_t pages_in_flight;  /* evicted pages still served from the device   */
 } sfa_pager_stats;
 
 /* Allocates the device pool (all layers, K and V), the host-pinned cold pool,
@@ -68,11 +70,17 @@ SFA_API void sfa_pager_destroy(sfa_pager *pager);
 
 /* Starts a step: sequence b gets the next n_tok[b] positions (0 <= n_tok[b] <=
  * page_size; host array).  Pages whose last position leaves the window are
- * evicted (device-to-host copy of every layer's K and V on `stream`) or
- * released, new pages are taken from the pool, and the device page tables,
+ * released (SFA_ATTEND_WINDOW) or evicted (lossless): a device-to-host copy of
+ * every layer's K and V runs on a copy stream of the pager's own, ordered after
+ * the work already on `stream`, and the page keeps serving reads from HBM until
+ * a later step sees the copy complete; only then does its table entry move to
+ * the cold page and the device page return to the pool.  An allocation that
+ * finds no other free page takes the oldest such page and makes `stream` wait
+ * for its copy.  New pages are taken from the pool, and the device page tables,
  * seq_len, kv_lo and the step's (seq, pos) token arrays are updated by a kernel
  * on `stream` (no host synchronisation).  Tokens of the step are ordered by
- * sequence, then position.  On error the pager is unchanged. */
+ * sequence, then position.  On error the pager is unchanged.  Host code: not
+ * for HIP graph capture (the per-layer calls below are). */
 SFA_API int sfa_pager_begin(sfa_pager *pager, const int32_t *n_tok, void *stream);
 
 /* Appends the step's tokens to one layer: k, v [n_tokens][n_head_kv][head_dim]
@@ -91,7 +99,10 @@ SFA_API int sfa_pager_rope_append(sfa_pager *pager, int32_t layer, float *q, con
  * f32 device, out [n_tokens][n_head * head_dim] f32 device.  A step with one
  * token per sequence runs sfa_attn_decode over the batch (split plan sized for
  * n_ctx when lossless, `window` when windowed); other steps run
- * sfa_attn_prefill per sequence (lossless only; Q8_0 needs head_dim >= 64). */
+ * sfa_attn_prefill per sequence with tokens (its limits: page_size a multiple
+ * of 64, Q8_0 with head_dim >= 64; otherwise SFA_ERR_UNSUPPORTED).  Under
+ * SFA_ATTEND_WINDOW a sequence may take at most one token in such a step (each
+ * token of a chunk would need its own window start): SFA_ERR_UNSUPPORTED. */
 SFA_API int sfa_pager_attend(sfa_pager *pager, int32_t layer, const float *q, float *out,
                              void *stream);
 
@@ -105,6 +116,15 @@ SFA_API int sfa_pager_desc(const sfa_pager *pager, int32_t layer, sfa_kv_desc *o
 
 /* Pages per sequence table row (ceil(n_ctx / page_size)). */
 SFA_API int32_t sfa_pager_max_pages(const sfa_pager *pager);
+
+/* The device arrays the pager keeps for libsfa: page tables [n_seq][max_pages],
+ * seq_len [n_seq] and kv_lo [n_seq] (int32, device memory owned by the pager,
+ * valid until sfa_pager_destroy; rewritten at every sfa_pager_begin on that
+ * call's stream).  For callers that run sfa.h entry points over the pager's
+ * pools themselves (sfa_attn_decode_split to time the split pass alone,
+ * sfa_attn_decode_noalloc).  Any pointer may be NULL. */
+SFA_API int sfa_pager_device_tables(const sfa_pager *pager, const int32_t **page_table,
+                                    const int32_t **seq_len, const int32_t **kv_lo);
 
 /* Host mirror of the page tables [n_seq][max_pages] and fill positions [n_seq];
  * either pointer may be NULL. */

@@ -148,6 +148,7 @@ HOST_EXPORTS = (
     "sfa_pager_stats_get",
     "sfa_pager_desc",
     "sfa_pager_max_pages",
+    "sfa_pager_device_tables",
     "sfa_pager_tables",
 )
 
@@ -178,6 +179,7 @@ class SfaPagerStats(ctypes.Structure):
         ("dev_pages_in_use", ctypes.c_int64),
         ("cold_pages_in_use", ctypes.c_int64),
         ("bytes_evicted", ctypes.c_int64),
+        ("pages_in_flight", ctypes.c_int64),
     ]
 
 
@@ -216,6 +218,8 @@ def load_host(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_pager_desc.restype = ctypes.c_int
     lib.sfa_pager_max_pages.argtypes = [P]
     lib.sfa_pager_max_pages.restype = i32
+    lib.sfa_pager_device_tables.argtypes = [P, ctypes.POINTER(P), ctypes.POINTER(P), ctypes.POINTER(P)]
+    lib.sfa_pager_device_tables.restype = ctypes.c_int
     lib.sfa_pager_tables.argtypes = [P, P, P]
     lib.sfa_pager_tables.restype = ctypes.c_int
     _host = lib

@@ -2,17 +2,25 @@
 //
 // Owns the device pool of every layer's K and V pages, the host-pinned cold
 // pool and the device page tables; PagePlanner decides residency and this file
-// carries its decisions out on one stream: eviction copies (one strided
-// device-to-host copy moves a page of every layer, K and V), then one small
-// kernel that applies the page-table edits and writes seq_len, kv_lo and the
-// step's (seq, pos) token arrays.  Step metadata travels as kernel arguments,
-// so a step needs no host staging buffer and no synchronisation.
+// carries its decisions out: eviction copies (one strided device-to-host copy
+// moves a page of every layer, K and V) run on a copy stream of the pager's
+// own, after an event marking the caller's stream at the step's start, so the
+// step's attention and appends do not wait for them.  An evicted page keeps
+// serving reads from HBM until its copy is seen complete (an event query at a
+// later step); then its table slot moves to the cold page and the device page
+// is reused.  Only an allocation that finds no other free page makes the
+// caller's stream wait for a copy.  One small kernel per step applies the
+// page-table edits and writes seq_len, kv_lo and the step's (seq, pos) token
+// arrays.  Step metadata travels as kernel arguments, so a step needs no host
+// staging buffer and no synchronisation.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
+#include <deque>
 #include <map>
 #include <new>
+#include <utility>
 #include <vector>
 
 #include "page_planner.h"
@@ -77,6 +85,12 @@ struct sfa_pager {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     std::vector<sfa_kv_desc> descs;
+    // deferred eviction: copies on copy_stream; one event per eviction in
+    // flight, in eviction order (the planner's in-flight order)
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t step_ready = nullptr;
+    std::deque<std::pair<uint64_t, hipEvent_t>> ev_flight;
+    std::vector<hipEvent_t> ev_free;
     // the current step
     std::vector<int32_t> step_ntok, step_pos0, step_off;
     int32_t step_tokens = 0;
@@ -86,9 +100,13 @@ struct sfa_pager {
     sfa_pager(const sfa_pager_config &c, int n_pages, int n_cold)
         : cfg(c),
           planner(c.n_seq, c.page_size, (uint32_t)c.n_ctx, (uint32_t)c.window, n_pages, n_cold,
-                  c.attend == SFA_ATTEND_LOSSLESS, c.seed) {}
+                  c.attend == SFA_ATTEND_LOSSLESS, c.seed, /*async_evict=*/true) {}
 
     ~sfa_pager() {
+        for (auto &e : ev_flight) (void)hipEventDestroy(e.second);
+        for (hipEvent_t e : ev_free) (void)hipEventDestroy(e);
+        if (step_ready) (void)hipEventDestroy(step_ready);
+        if (copy_stream) (void)hipStreamDestroy(copy_stream);
         if (dev_pool) (void)hipFree(dev_pool);
         if (cold_pool) (void)hipHostFree(cold_pool);
         for (int32_t *p : {d_table, d_seq_len, d_kv_lo, d_tok_seq, d_tok_pos})
@@ -129,25 +147,83 @@ struct sfa_pager {
         return SFA_OK;
     }
 
+    // Evictions whose copies have completed, counted from the oldest (the
+    // planner retires in the same order); -1 on a runtime error.
+    int completed_evictions() const {
+        int done = 0;
+        for (const auto &e : ev_flight) {
+            const hipError_t q = hipEventQuery(e.second);
+            if (q == hipErrorNotReady) break;
+            if (q != hipSuccess) return -1;
+            ++done;
+        }
+        return done;
+    }
+
+    // Carries out a step's actions on stream s (copies on copy_stream).  The
+    // event bookkeeping changes only when every call succeeded.
     int apply(const std::vector<sfa::PageAction> &actions, hipStream_t s) {
         const size_t slab = (size_t)2 * cfg.n_layer;  // (layer, K|V) rows of a page
         std::map<int32_t, int32_t> edits;              // table slot -> final id
+        std::deque<std::pair<uint64_t, hipEvent_t>> flight = ev_flight;
+        std::vector<hipEvent_t> spare = ev_free, created, released;
+        bool marked = false;
+        int64_t copied = 0;
+        auto fail = [&](int rc) {
+            for (hipEvent_t e : created) (void)hipEventDestroy(e);
+            return rc;
+        };
         for (const sfa::PageAction &a : actions) {
             if (a.kind == sfa::PageAction::kEvict) {
+                // the copy follows everything issued on s so far (the page's
+                // writes included): s marks the step, copy_stream waits for it
+                if (!marked) {
+                    if (hipEventRecord(step_ready, s) != hipSuccess ||
+                        hipStreamWaitEvent(copy_stream, step_ready, 0) != hipSuccess)
+                        return fail(SFA_ERR_RUNTIME);
+                    marked = true;
+                }
                 // page `dev` of every (layer, K|V) pool -> cold page `cold`
                 if (hipMemcpy2DAsync(cold_pool + (size_t)a.cold * page_bytes,
                                      (size_t)n_cold() * page_bytes,
                                      dev_pool + (size_t)a.dev * page_bytes,
                                      (size_t)n_pages() * page_bytes, page_bytes, slab,
-                                     hipMemcpyDeviceToHost, s) != hipSuccess)
-                    return SFA_ERR_RUNTIME;
-                bytes_evicted += (int64_t)(page_bytes * slab);
+                                     hipMemcpyDeviceToHost, copy_stream) != hipSuccess)
+                    return fail(SFA_ERR_RUNTIME);
+                hipEvent_t ev = nullptr;
+                if (!spare.empty()) {
+                    ev = spare.back();
+                    spare.pop_back();
+                } else {
+                    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+                        return fail(SFA_ERR_RUNTIME);
+                    created.push_back(ev);
+                }
+                if (hipEventRecord(ev, copy_stream) != hipSuccess) return fail(SFA_ERR_RUNTIME);
+                flight.emplace_back(a.evict, ev);
+                copied += (int64_t)(page_bytes * slab);
+            } else if (a.kind == sfa::PageAction::kRetire) {
+                // retirements pop the oldest eviction in flight
+                if (flight.empty() || flight.front().first != a.evict) return fail(SFA_ERR_RUNTIME);
+                if (a.wait && hipStreamWaitEvent(s, flight.front().second, 0) != hipSuccess)
+                    return fail(SFA_ERR_RUNTIME);
+                released.push_back(flight.front().second);
+                flight.pop_front();
             }
-            const int32_t slot = a.seq * max_pages + a.lpage;
-            edits[slot] = planner.table()[slot];
+            if (a.edit) {
+                const int32_t slot = a.seq * max_pages + a.lpage;
+                edits[slot] = planner.table()[slot];
+            }
         }
         std::vector<std::pair<int32_t, int32_t>> list(edits.begin(), edits.end());
-        return launch_updates(list, s);
+        if (const int rc = launch_updates(list, s); rc != SFA_OK) return fail(rc);
+        // commit: an event released here may be re-recorded later, after the
+        // waits already enqueued on it
+        spare.insert(spare.end(), released.begin(), released.end());
+        ev_flight.swap(flight);
+        ev_free.swap(spare);
+        bytes_evicted += copied;
+        return SFA_OK;
     }
 };
 
@@ -234,6 +310,10 @@ SFA_API int sfa_pager_create(const sfa_pager_config *cfg_in, sfa_pager **out) {
     p->ws_bytes = sfa_decode_workspace_bytes(&p->descs[0], c.n_seq, p->max_span);
     if (p->ws_bytes == 0) return fail(SFA_ERR_INVALID_ARGUMENT);
     if (hipMalloc(&p->ws, p->ws_bytes) != hipSuccess) return fail(SFA_ERR_OUT_OF_MEMORY);
+    // default-priority copy stream and the step marker of deferred eviction
+    if (hipStreamCreateWithFlags(&p->copy_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&p->step_ready, hipEventDisableTiming) != hipSuccess)
+        return fail(SFA_ERR_RUNTIME);
     if (sfa_workspace_init(p->ws, p->ws_bytes, nullptr) != SFA_OK) return fail(SFA_ERR_RUNTIME);
     if (hipDeviceSynchronize() != hipSuccess) return fail(SFA_ERR_RUNTIME);
     *out = p;
@@ -251,28 +331,48 @@ SFA_API int sfa_pager_begin(sfa_pager *p, const int32_t *n_tok, void *stream) {
     const int n_seq = p->cfg.n_seq;
     for (int b = 0; b < n_seq; ++b)
         if (n_tok[b] < 0 || n_tok[b] > p->cfg.page_size) return SFA_ERR_INVALID_ARGUMENT;
-    std::vector<sfa::PageAction> actions;
+    const int done = p->completed_evictions();
+    if (done < 0) return SFA_ERR_RUNTIME;
     try {
-        const sfa::PagePlanner saved = p->planner;
-        int32_t off = 0;
+        // everything below is undone on any error: the planner is restored
+        // from this copy and the step metadata is committed last
+        sfa::PagePlanner saved = p->planner;
+        std::vector<int32_t> pos0(n_seq), off(n_seq);
+        int32_t total = 0;
         for (int b = 0; b < n_seq; ++b) {
-            p->step_pos0[b] = (int32_t)p->planner.store(b).used();
-            p->step_off[b] = off;
-            p->step_ntok[b] = n_tok[b];
-            off += n_tok[b];
-            if (int rc = p->planner.plan(b, n_tok[b], &actions); rc != SFA_OK) {
-                p->planner = saved;
-                p->step_open = false;
-                return rc;
+            pos0[b] = (int32_t)p->planner.store(b).used();
+            off[b] = total;
+            total += n_tok[b];
+        }
+        std::vector<sfa::PageAction> actions;
+        int rc = SFA_OK;
+        try {
+            p->planner.retire_completed(done, &actions);
+        } catch (const std::bad_alloc &) {
+            rc = SFA_ERR_OUT_OF_MEMORY;
+        }
+        if (rc == SFA_OK) rc = p->planner.plan_step(n_tok, &actions);
+        if (rc == SFA_OK) {
+            // apply() reads the step metadata for the update kernel
+            std::vector<int32_t> old_ntok(n_tok, n_tok + n_seq);
+            p->step_ntok.swap(old_ntok);
+            p->step_pos0.swap(pos0);
+            p->step_off.swap(off);
+            rc = p->apply(actions, as_stream(stream));
+            if (rc != SFA_OK) {
+                p->step_ntok.swap(old_ntok);
+                p->step_pos0.swap(pos0);
+                p->step_off.swap(off);
             }
         }
-        p->step_tokens = off;
-    } catch (const std::bad_alloc &) {
-        return SFA_ERR_OUT_OF_MEMORY;
-    }
-    p->step_open = true;
-    try {
-        return p->apply(actions, as_stream(stream));
+        if (rc != SFA_OK) {
+            p->planner = std::move(saved);
+            p->step_open = false;
+            return rc;
+        }
+        p->step_tokens = total;
+        p->step_open = true;
+        return SFA_OK;
     } catch (const std::bad_alloc &) {  // no exception leaves the C ABI
         return SFA_ERR_OUT_OF_MEMORY;
     } catch (...) {
@@ -311,13 +411,18 @@ SFA_API int sfa_pager_attend(sfa_pager *p, int32_t layer, const float *q, float 
         return sfa_attn_decode(d, q, out, p->d_table, p->max_pages, p->d_seq_len,
                                windowed ? p->d_kv_lo : nullptr, p->cfg.n_seq, p->max_span, scale,
                                p->ws, p->ws_bytes, stream);
-    if (windowed) return SFA_ERR_UNSUPPORTED;  // per-query windows in a chunk
+    // a chunk (or a batch with idle sequences): the causal prefill per active
+    // sequence.  Under the sliding window one token attends [attend_lo, pos];
+    // the tokens of a longer chunk would each need their own window start.
     const size_t row = (size_t)p->cfg.n_head * p->cfg.head_dim;
+    for (int b = 0; b < p->cfg.n_seq; ++b)
+        if (windowed && p->step_ntok[b] > 1) return SFA_ERR_UNSUPPORTED;
     for (int b = 0; b < p->cfg.n_seq; ++b) {
         if (p->step_ntok[b] == 0) continue;
         const size_t off = (size_t)p->step_off[b] * row;
+        const int32_t lo = windowed ? (int32_t)p->planner.attend_lo(b) : 0;
         const int rc = sfa_attn_prefill(d, q + off, out + off, p->d_table + (size_t)b * p->max_pages,
-                                        p->max_pages, p->step_pos0[b], p->step_ntok[b], 0, scale,
+                                        p->max_pages, p->step_pos0[b], p->step_ntok[b], lo, scale,
                                         stream);
         if (rc != SFA_OK) return rc;
     }
@@ -355,6 +460,7 @@ SFA_API int sfa_pager_stats_get(const sfa_pager *p, sfa_pager_stats *out) {
     out->dev_pages_in_use = s.dev_in_use;
     out->cold_pages_in_use = s.cold_in_use;
     out->bytes_evicted = p->bytes_evicted;
+    out->pages_in_flight = s.in_flight;
     return SFA_OK;
 }
 
@@ -366,6 +472,15 @@ SFA_API int sfa_pager_desc(const sfa_pager *p, int32_t layer, sfa_kv_desc *out) 
 }
 
 SFA_API int32_t sfa_pager_max_pages(const sfa_pager *p) { return p ? p->max_pages : 0; }
+
+SFA_API int sfa_pager_device_tables(const sfa_pager *p, const int32_t **page_table,
+                                    const int32_t **seq_len, const int32_t **kv_lo) {
+    if (p == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+    if (page_table) *page_table = p->d_table;
+    if (seq_len) *seq_len = p->d_seq_len;
+    if (kv_lo) *kv_lo = p->d_kv_lo;
+    return SFA_OK;
+}
 
 SFA_API int sfa_pager_tables(const sfa_pager *p, int32_t *page_table, int32_t *used) {
     if (p == nullptr) return SFA_ERR_INVALID_ARGUMENT;

@@ -10,7 +10,7 @@
 // reference semantics: engine.cpp:2620-2661 copies the evicted column to the
 // RAM cold store before the write) or dropped (opt-in sliding window, whose
 // attention never reads it again).  The planner only decides; the caller
-// executes the returned actions (copies, table edits) in order.
+// executes the returned actions (copies, waits, table edits) in order.
 #pragma once
 
 #include <cstddef>
@@ -47,21 +47,32 @@ private:
     uint32_t used_ = 0;
 };
 
+// With deferred eviction (PagePlanner's async_evict) a page that leaves the
+// window is copied to its cold page while its table slot still names the device
+// page (the data is the same, and attention may read either); kRetire later
+// points the slot at the cold page and frees the device page, once the copy is
+// known complete (retire_completed) or, when an allocation needs the page,
+// at once with `wait` set: the caller then orders its later work after that
+// copy.  Without it, kEvict edits the slot and frees the page immediately.
 struct PageAction {
-    enum Kind : int { kAlloc = 0, kEvict = 1, kDrop = 2 };
+    enum Kind : int { kAlloc = 0, kEvict = 1, kDrop = 2, kRetire = 3 };
     Kind kind;
     int32_t seq;
-    int32_t lpage;  // logical page of the sequence
-    int32_t dev;    // device page (allocated, or released by kEvict / kDrop)
-    int32_t cold;   // cold page written by kEvict, else -1
+    int32_t lpage;    // logical page of the sequence
+    int32_t dev;      // device page (allocated, or released by kEvict / kDrop / kRetire)
+    int32_t cold;     // cold page written by kEvict / named by kRetire, else -1
+    uint64_t evict;   // kEvict / kRetire: the eviction's serial number
+    bool wait;        // kRetire: the copy may still be in flight
+    bool edit;        // the action changes the table slot (seq, lpage)
 };
 
 struct PlannerStats {
     int64_t allocated = 0;   // device pages handed out
     int64_t evicted = 0;     // pages moved to the cold pool
     int64_t dropped = 0;     // pages released without a copy (sliding window)
-    int64_t dev_in_use = 0;
+    int64_t dev_in_use = 0;  // device pages held (evictions in flight included)
     int64_t cold_in_use = 0;
+    int64_t in_flight = 0;   // evictions whose device page is not yet retired
 };
 
 class PagePlanner {
@@ -70,15 +81,29 @@ public:
     // (evicted pages are dropped).  A sequence holds at most
     // ceil(window / page_size) + 1 device pages.
     PagePlanner(int n_seq, int page_size, uint32_t n_ctx, uint32_t window, int n_pages,
-                int n_cold_pages, bool keep_cold, uint64_t seed);
+                int n_cold_pages, bool keep_cold, uint64_t seed, bool async_evict = false);
 
     // Plans writing positions [used, used + n_tok) of sequence `seq`, in order,
     // and advances its KvStore.  n_tok <= page_size.  Returns 0 or an sf_status
-    // code (1 invalid argument, 4 out of memory); on error nothing changes.
+    // code (1 invalid argument, 4 out of memory).  On error the planner may be
+    // partly advanced: callers restore a copy taken before (see plan_step).
     int plan(int seq, int n_tok, std::vector<PageAction> *actions);
 
-    // Releases every page of a sequence and rewinds it to position 0.
+    // plan() for every sequence of a step (n_tok[n_seq]), all or nothing: on
+    // any error, an exception included, the planner is left as it was and
+    // `actions` as it came in.  Never throws.
+    int plan_step(const int32_t *n_tok, std::vector<PageAction> *actions) noexcept;
+
+    // Retires the `n` oldest evictions in flight (their copies are known
+    // complete): kRetire actions without wait.
+    void retire_completed(int n, std::vector<PageAction> *actions);
+
+    // Releases every page of a sequence and rewinds it to position 0.  A page
+    // whose eviction is still in flight stays held until it is retired.
     void reset(int seq, std::vector<PageAction> *actions);
+
+    // Serial numbers of the evictions in flight, oldest first.
+    std::vector<uint64_t> in_flight() const;
 
     int n_seq() const { return (int)stores_.size(); }
     int page_size() const { return page_size_; }
@@ -91,13 +116,23 @@ public:
     uint32_t attend_lo(int seq) const;
 
 private:
-    int32_t take_device_page();
+    struct Pending {
+        int32_t seq, lpage, dev, cold;
+        uint64_t evict;
+        bool orphan;  // the sequence was reset: no table edit at retirement
+    };
+
+    int32_t take_device_page(std::vector<PageAction> *actions);
     int32_t take_cold_page();
     uint64_t next_random();
+    void retire_front(bool wait, std::vector<PageAction> *actions);
 
     int page_size_;
     int max_pages_;
     bool keep_cold_;
+    bool async_;
+    uint64_t next_evict_ = 0;
+    std::vector<Pending> pending_;  // evictions in flight, oldest first
     std::vector<KvStore> stores_;
     std::vector<int32_t> table_;
     std::vector<int32_t> free_dev_;

@@ -38,6 +38,7 @@ class KvPager:
         self._h = h
         self.n_layer, self.n_head, self.n_head_kv, self.head_dim = n_layer, n_head, n_head_kv, head_dim
         self.n_seq, self.n_ctx, self.page_size, self.attend_mode = n_seq, n_ctx, page_size, attend
+        self.window = window if 0 < window <= n_ctx else n_ctx
         self.max_pages = int(lib.sfa_pager_max_pages(h))
         self.n_tok = np.zeros(n_seq, dtype=np.int32)
 
@@ -105,6 +106,19 @@ class KvPager:
         d = _lib.SfaKvDesc()
         _lib.check(_lib.load_host().sfa_pager_desc(self._h, layer, ctypes.byref(d)), "desc")
         return d
+
+    def device_tables(self) -> tuple[int, int, int]:
+        """Device addresses of the pager's page tables [n_seq, max_pages],
+        seq_len [n_seq] and kv_lo [n_seq] (int32)."""
+        pt, sl, lo = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(_lib.load_host().sfa_pager_device_tables(self._h, ctypes.byref(pt), ctypes.byref(sl),
+                                                            ctypes.byref(lo)), "device_tables")
+        return pt.value, sl.value, lo.value
+
+    @property
+    def max_span(self) -> int:
+        """The max_seq_len the pager's decode passes: n_ctx, or the window."""
+        return self.window if self.attend_mode == SFA_ATTEND_WINDOW else self.n_ctx
 
     def tables(self) -> tuple[np.ndarray, np.ndarray]:
         """Host mirror: page tables [n_seq, max_pages] and fill positions [n_seq]."""

@@ -11,10 +11,23 @@
 // of pages changes nothing.
 #include <cstdio>
 #include <cstdlib>
+#include <new>
 #include <set>
 #include <vector>
 
 #include "page_planner.h"
+
+// Allocation failure injection for the all-or-nothing checks: when
+// g_fail_countdown reaches zero, the next operator new throws.
+static long g_fail_countdown = -1;
+
+void *operator new(std::size_t n) {
+    if (g_fail_countdown >= 0 && g_fail_countdown-- == 0) throw std::bad_alloc();
+    if (void *p = std::malloc(n ? n : 1)) return p;
+    throw std::bad_alloc();
+}
+void operator delete(void *p) noexcept { std::free(p); }
+void operator delete(void *p, std::size_t) noexcept { std::free(p); }
 
 static int g_checks = 0;
 #define CHECK(c)                                                              \
@@ -183,6 +196,145 @@ static void test_out_of_pages_is_atomic() {
     CHECK(acts[0].dev == acts[1].dev);
 }
 
+// Deferred eviction: the evicted page's slot keeps its device page until the
+// eviction is retired; then it names the cold page and the device page is free.
+// Completed copies retire in eviction order; an allocation that finds no free
+// page retires the oldest in-flight eviction at once (wait set).
+static void test_deferred_eviction() {
+    const int n_seq = 3, P = 32;
+    const uint32_t n_ctx = 2048, W = 100;
+    const int win_pages = (W + P - 1) / P + 1;
+    for (int slack : {0, 2}) {
+        const int n_pages = n_seq * win_pages + slack;
+        PagePlanner pl(n_seq, P, n_ctx, W, n_pages, n_seq * 64, true, 11, true);
+        PagePlanner sync(n_seq, P, n_ctx, W, n_pages, n_seq * 64, true, 11, false);
+        std::vector<PageAction> acts;
+        std::set<uint64_t> issued;
+        int waits = 0, retired = 0;
+        for (int step = 0; step < 200; ++step) {
+            int32_t n_tok[n_seq];
+            for (int b = 0; b < n_seq; ++b) {
+                n_tok[b] = (step < 6 ? 30 : 1) + (b == 1 && step % 5 == 0);
+                if (!pl.store(b).can_fit(n_tok[b])) n_tok[b] = 0;
+            }
+            // copies known complete: every eighth step, all those in flight
+            // or half of them
+            acts.clear();
+            const std::vector<uint64_t> fl = pl.in_flight();
+            const int done = step % 8 == 7 ? (int)fl.size() : step % 8 == 3 ? (int)fl.size() / 2 : 0;
+            pl.retire_completed(done, &acts);
+            CHECK((int)acts.size() == std::min<int>(done, (int)fl.size()));
+            for (size_t i = 0; i < acts.size(); ++i) {
+                CHECK(acts[i].kind == PageAction::kRetire && !acts[i].wait && acts[i].evict == fl[i]);
+                ++retired;
+            }
+            acts.clear();
+            CHECK(pl.plan_step(n_tok, &acts) == 0);
+            std::vector<PageAction> sacts;
+            CHECK(sync.plan_step(n_tok, &sacts) == 0);
+            for (const PageAction &a : acts) {
+                if (a.kind == PageAction::kEvict) {
+                    CHECK(!a.edit && issued.insert(a.evict).second);
+                } else if (a.kind == PageAction::kRetire) {
+                    CHECK(a.wait && issued.count(a.evict) == 1);  // issued before, maybe this step
+                    ++waits;
+                    ++retired;
+                }
+            }
+            // same logical bookkeeping as immediate eviction, and every page
+            // out of the window is cold or still in flight on its device page
+            const std::vector<uint64_t> now = pl.in_flight();
+            CHECK(pl.stats().in_flight == (int64_t)now.size());
+            CHECK(pl.stats().evicted == sync.stats().evicted);
+            CHECK(pl.stats().cold_in_use == sync.stats().cold_in_use);
+            std::set<int32_t> dev;
+            for (int b = 0; b < n_seq; ++b) {
+                CHECK(pl.store(b).used() == sync.store(b).used());
+                for (int lp = 0; lp < pl.max_pages(); ++lp) {
+                    const size_t i = (size_t)b * pl.max_pages() + lp;
+                    const int32_t a = pl.table()[i], y = sync.table()[i];
+                    if (y >= 0) {
+                        CHECK(a >= 0);  // resident in both (placement may differ)
+                    } else if (y == -1) {
+                        CHECK(a == -1);
+                    } else {
+                        CHECK(a <= -2 || a >= 0);  // cold, or device page in flight
+                    }
+                    if (a >= 0) CHECK(dev.insert(a).second);
+                }
+            }
+            CHECK((int)dev.size() <= n_pages);
+            CHECK((int64_t)dev.size() <= pl.stats().dev_in_use);
+        }
+        CHECK(retired + (int)pl.in_flight().size() == (int)issued.size() && !issued.empty());
+        // an exact pool must retire in-flight pages to allocate
+        if (slack == 0) CHECK(waits > 0);
+        // retiring everything gives the immediate-eviction tables
+        acts.clear();
+        pl.retire_completed((int)pl.in_flight().size(), &acts);
+        for (int b = 0; b < n_seq; ++b)
+            for (int lp = 0; lp < pl.max_pages(); ++lp) {
+                const size_t i = (size_t)b * pl.max_pages() + lp;
+                CHECK((pl.table()[i] <= -2) == (sync.table()[i] <= -2));
+                CHECK((pl.table()[i] == -1) == (sync.table()[i] == -1));
+            }
+        CHECK(pl.stats().in_flight == 0 && pl.stats().dev_in_use == sync.stats().dev_in_use);
+    }
+}
+
+// A reset while a sequence's eviction is in flight: the slot is cleared at
+// once, the cold page released, and the later retirement edits nothing.
+static void test_reset_with_eviction_in_flight() {
+    PagePlanner pl(2, 32, 512, 64, 8, 32, true, 5, true);
+    std::vector<PageAction> acts;
+    const int32_t fill[2] = {32, 32};
+    for (int i = 0; i < 3; ++i) CHECK(pl.plan_step(fill, &acts) == 0);
+    const int32_t one[2] = {1, 1};
+    acts.clear();
+    CHECK(pl.plan_step(one, &acts) == 0);  // position 96: page 0 of each leaves the window
+    CHECK(pl.in_flight().size() == 2 && pl.stats().cold_in_use == 2);
+    acts.clear();
+    pl.reset(1, &acts);
+    CHECK(pl.stats().cold_in_use == 1 && pl.stats().in_flight == 2);
+    for (int lp = 0; lp < pl.max_pages(); ++lp) CHECK(pl.table()[(size_t)pl.max_pages() + lp] == -1);
+    acts.clear();
+    pl.retire_completed(2, &acts);
+    CHECK(acts.size() == 2 && acts[0].edit && !acts[1].edit);
+    CHECK(pl.table()[0] <= -2 && pl.stats().in_flight == 0);
+}
+
+// plan_step is all or nothing, whatever allocation fails inside it.
+static void test_plan_step_all_or_nothing() {
+    for (bool async : {false, true}) {
+        for (long k = 0;; ++k) {
+            PagePlanner pl(3, 32, 1024, 64, 3 * 4, 3 * 32, true, 9, async);
+            std::vector<PageAction> acts;
+            const int32_t warm[3] = {32, 20, 32};
+            for (int i = 0; i < 4; ++i) CHECK(pl.plan_step(warm, &acts) == 0);
+            const std::vector<int32_t> table = pl.table();
+            const std::vector<uint64_t> fl = pl.in_flight();
+            const uint32_t used[3] = {pl.store(0).used(), pl.store(1).used(), pl.store(2).used()};
+            const int64_t ev = pl.stats().evicted, al = pl.stats().allocated;
+            acts.assign(3, PageAction{});
+            const int32_t step[3] = {32, 32, 31};
+            g_fail_countdown = k;
+            const int rc = pl.plan_step(step, &acts);
+            const bool failed = g_fail_countdown < 0;
+            g_fail_countdown = -1;
+            if (rc == 0) {
+                CHECK(!failed && pl.store(0).used() == used[0] + 32);
+                break;
+            }
+            CHECK(rc == 4 && failed);
+            CHECK(acts.size() == 3 && pl.table() == table && pl.in_flight() == fl);
+            CHECK(pl.store(0).used() == used[0] && pl.store(1).used() == used[1] &&
+                  pl.store(2).used() == used[2]);
+            CHECK(pl.stats().evicted == ev && pl.stats().allocated == al);
+            CHECK(k < 10000);
+        }
+    }
+}
+
 int main() {
     test_kv_store();
     test_planner_lossless(true);
@@ -190,6 +342,9 @@ int main() {
     test_no_paging_when_window_covers_ctx();
     test_seeded_placement();
     test_out_of_pages_is_atomic();
+    test_deferred_eviction();
+    test_reset_with_eviction_in_flight();
+    test_plan_step_all_or_nothing();
     std::printf("ok %d\n", g_checks);
     return 0;
 }

@@ -125,7 +125,8 @@ def test_pager_lossless_bit_identical(gpu, oracle_mod, kv_type):
     assert st["bytes_evicted"] == evicted_pages * 2 * 2 * 256 * 8 * row
     assert st["dev_pages_in_use"] <= 4 * 5
     pt, used = m.pager.tables()
-    assert (used == lens).all() and (pt <= -2).sum() == evicted_pages
+    # pages whose copy was not yet seen complete still name their device page
+    assert (used == lens).all() and (pt <= -2).sum() + st["pages_in_flight"] == evicted_pages
     # and the paged result is the reference attention over every position
     q, out = outs[0]
     ref = host.attention(q.cpu().numpy(), 32, m.host_pt, lens.astype(np.int32), None,
@@ -187,9 +188,10 @@ def test_pager_out_of_pages_and_reset(gpu):
 @pytest.mark.parametrize("attend", [SFA_ATTEND_WINDOW, SFA_ATTEND_LOSSLESS])
 def test_pager_window_4096_history_65536(gpu, attend):
     # the KV-window workload: 4 sequences, 65536-token histories, W = 4096,
-    # device pool sized to the window (4 * 17 pages), then decode steps
-    steps = 128 if attend == SFA_ATTEND_WINDOW else 8
-    m = Mirror(n_seq=4, n_ctx=65536 + 256, window=4096, attend=attend, n_layer=1, seed=4)
+    # device pool sized to the window (4 * 17 pages), then 128 decode steps
+    # (two layers); paged == full-resident bit for bit (test_kv_paging.cpp:242-248)
+    steps = 128
+    m = Mirror(n_seq=4, n_ctx=65536 + 256, window=4096, attend=attend, n_layer=2, seed=4)
     m.fill([65536 - 37, 65536 - 300, 65536 - 1, 65536 - 129])
     _decode_and_compare(m, steps, check_every=16)
     st = m.pager.stats()
@@ -237,3 +239,70 @@ def test_pager_rope_append_matches_full(gpu):
             torch.cuda.synchronize()
             assert torch.equal(out, ref), f"step {step}: paged != full-resident"
     assert pager.stats()["pages_evicted"] > 0
+
+
+def test_pager_deferred_eviction_serves_pages_in_flight(gpu):
+    # an evicted page keeps serving reads from HBM until its copy is seen
+    # complete; a pool with no spare page retires in-flight pages at once
+    # (the stream waits for the copy); both stay bit-identical to full residency
+    for n_pages, seed in ((0, 21), (4 * 5 + 6, 22)):  # the default (tight) pool, then 6 spare pages
+        m = Mirror(n_seq=4, n_ctx=4096, window=1024, attend=SFA_ATTEND_LOSSLESS, n_layer=2, seed=seed)
+        if n_pages:
+            m.pager.close()
+            m.pager = KvPager(n_layer=2, n_head=32, n_head_kv=8, head_dim=128, kv_type=SFA_KV_F16,
+                              page_size=256, n_seq=4, n_ctx=4096, window=1024,
+                              attend=SFA_ATTEND_LOSSLESS, n_pages=n_pages, seed=seed)
+        m.fill([1200, 1279, 1500, 1023])
+        seen_in_flight = 0
+        for s in range(300):
+            outs = m.step(np.ones(4, np.int32))
+            st = m.pager.stats()
+            pt, used = m.pager.tables()
+            assert (pt <= -2).sum() + st["pages_in_flight"] == st["pages_evicted"]
+            seen_in_flight = max(seen_in_flight, st["pages_in_flight"])
+            if s % 13 == 0 or s == 299:
+                for layer, (q, out) in enumerate(outs):
+                    ref = m.full_decode(layer, q)
+                    torch.cuda.synchronize()
+                    assert torch.equal(out, ref), f"pool {n_pages} step {s} layer {layer}"
+        assert st["pages_evicted"] > 0 and seen_in_flight > 0
+        m.pager.close()
+
+
+def test_pager_page_size_32(gpu, oracle_mod):
+    # 32-position pages: decode steps run; a multi-token step appends but its
+    # attention (the prefill, 64-position tiles) is refused, with no change
+    host = oracle_mod.HostPagedKv(8, 128, 32, SFA_KV_F16, 2 * 64 + 2)
+    m = Mirror(n_seq=2, n_ctx=2048, window=300, attend=SFA_ATTEND_LOSSLESS, page_size=32, seed=23,
+               oracle=host)
+    m.fill([500, 333])
+    outs = _decode_and_compare(m, 40, check_every=9)
+    q, out = outs[0]
+    ref = host.attention(q.cpu().numpy(), 32, m.host_pt, m.used.astype(np.int32), None,
+                         mode=oracle_mod.GGML).reshape(2, -1)
+    assert_close(out.cpu().numpy(), ref, what="page size 32 vs oracle")
+    assert m.pager.begin(np.array([2, 1], np.int32)) == 0
+    q = torch.randn((3, 32, 128), device="cuda")
+    from strataflow_amd import _lib
+    with pytest.raises(_lib.SfaError) as e:
+        m.pager.attend(0, q)
+    assert e.value.status == _lib.SFA_ERR_UNSUPPORTED
+
+
+def test_pager_window_idle_sequence(gpu, oracle_mod):
+    # sliding window with an idle sequence in the step: the active ones attend
+    # their own window (one token each, through the causal prefill)
+    host = oracle_mod.HostPagedKv(8, 128, 256, SFA_KV_F16, 3 * 16 + 2)
+    m = Mirror(n_seq=3, n_ctx=4096, window=700, attend=SFA_ATTEND_WINDOW, seed=24, oracle=host)
+    m.fill([1500, 900, 2000])
+    for s in range(5):
+        n_tok = np.array([1, 0, 1] if s % 2 == 0 else [0, 1, 1], np.int32)
+        outs = m.step(n_tok)
+        q, out = outs[0]
+        act = np.nonzero(n_tok)[0]
+        used = m.used.astype(np.int32)
+        lo = np.maximum(used - 700, 0).astype(np.int32)
+        qa = q.cpu().numpy()
+        ref = host.attention(qa, 32, m.host_pt[act], used[act], lo[act],
+                             mode=oracle_mod.GGML).reshape(len(act), -1)
+        assert_close(out.cpu().numpy(), ref, what=f"idle step {s}")

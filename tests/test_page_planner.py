@@ -36,7 +36,7 @@ def test_pager_config_layout():
     # the ctypes mirror of sfa_pager_config: 12 int32 then a uint64
     assert ctypes.sizeof(_lib.SfaPagerConfig) == 12 * 4 + 8
     assert _lib.SfaPagerConfig.seed.offset == 48
-    assert ctypes.sizeof(_lib.SfaPagerStats) == 6 * 8
+    assert ctypes.sizeof(_lib.SfaPagerStats) == 7 * 8
 
 
 def test_pager_rejects_bad_config():
