@@ -150,7 +150,11 @@ SFA_API int sfa_workspace_init(void *workspace, size_t ws_bytes, void *stream);
  *   scale : 1/sqrt(head_dim) in the reference (engine.cpp:1756)
  * Split-K over logical positions, then a merge pass in split order: results
  * do not depend on where pages live (paged == contiguous, bit for bit).
- * Sequences with seq_len <= kv_lo produce zeros. */
+ * Sequences with seq_len <= kv_lo produce zeros.  The kernels read seq_len on
+ * the device and never past the table: positions at or beyond
+ * max_pages * page_size are not attended (seq_len is clamped to the table's
+ * capacity without an error, which a device-side call cannot report);
+ * sfa_page_table_check() rejects such a table on the host. */
 SFA_API int sfa_attn_decode(const sfa_kv_desc *kv, const float *q, float *out,
                             const int32_t *page_table, int32_t max_pages,
                             const int32_t *seq_len, const int32_t *kv_lo,
@@ -200,7 +204,9 @@ SFA_API int sfa_attn_decode_noalloc(const sfa_kv_desc *kv, const float *q, float
  * positions kv_lo .. q_pos0+t (causal -INF mask above the diagonal, the
  * llama.cpp kq_mask convention).  q: [T][n_head][head_dim] f32,
  * out: [T][n_head * head_dim] f32.  F32, F16 and Q8_0 caches (Q8_0 with
- * head_dim >= 64, as in decode). */
+ * head_dim >= 64, as in decode).  The 64-position K/V tiles must each lie in
+ * one page: page_size must be a multiple of 64 (SFA_ERR_UNSUPPORTED
+ * otherwise). */
 SFA_API int sfa_attn_prefill(const sfa_kv_desc *kv, const float *q, float *out,
                              const int32_t *page_table, int32_t max_pages,
                              int32_t q_pos0, int32_t T, int32_t kv_lo,

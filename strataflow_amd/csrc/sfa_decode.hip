@@ -200,7 +200,8 @@ __device__ inline PlanRaw plan_load(const DecodeParams &p, int lane) {
 // Sequence b = -1 asks for the owner of row slot j (false: the slot is idle);
 // b >= 0 asks for sequence b's splits and first slot (the merge pass).  Every
 // lane of the wave must be active.  2 <= B <= 64: lane l computes sequence l;
-// larger batches walk the sequences wave-uniformly (slow path).
+// larger batches take ceil(B / 64) rounds of the same lane-parallel sums and
+// scans (lane l of round r holds sequence 64r + l).
 __device__ inline bool plan_lanes(const DecodeParams &p, const PlanRaw &raw, int j, int b, int lane, SlotPlan &sp) {
     sp = SlotPlan{0, 0, 0, 0, SeqGeom{0, 0, 0, 0}};
     const int cap = p.max_pages * p.page_size;
@@ -234,25 +235,44 @@ __device__ inline bool plan_lanes(const DecodeParams &p, const PlanRaw &raw, int
         sp.split = j - sp.rec0;
         return true;
     }
+    // more than 64 sequences: rounds of 64, lane l holding sequence 64r + l
+    // (coalesced loads); T and Z first, then the slot prefix round by round
+    const int rounds = (p.n_seq + kWave - 1) / kWave;
+    auto geom = [&](int r) -> SeqGeom {
+        const int bb = r * kWave + lane;
+        return bb < p.n_seq ? seq_geom(p.seq_len[bb], p.kv_lo ? p.kv_lo[bb] : 0, cap) : SeqGeom{0, 0, 0, 0};
+    };
     int T = 0, Z = 0;
-    for (int bb = 0; bb < p.n_seq; ++bb) {
-        const SeqGeom gb = seq_geom(p.seq_len[bb], p.kv_lo ? p.kv_lo[bb] : 0, cap);
-        T += gb.n_tiles;
-        Z += gb.n_tiles > 0;
+    for (int r = 0; r < rounds; ++r) {
+        const SeqGeom g = geom(r);
+        T += lane_sum_i(g.n_tiles);
+        Z += __popcll(__ballot(g.n_tiles > 0));
     }
-    int pre = 0;
-    for (int bb = 0; bb < p.n_seq; ++bb) {
-        const SeqGeom gb = seq_geom(p.seq_len[bb], p.kv_lo ? p.kv_lo[bb] : 0, cap);
-        const int nb = splits_of(gb.n_tiles, row - Z, T);
-        if (b >= 0 ? bb == b : j < pre + nb) {
-            sp.b = bb;
-            sp.n_b = nb;
-            sp.rec0 = pre;
-            sp.g = gb;
-            sp.split = j - pre;
+    int pre = 0;  // slots of the earlier rounds
+    for (int r = 0; r < rounds; ++r) {
+        const SeqGeom g = geom(r);
+        const int n_lane = splits_of(g.n_tiles, row - Z, T);
+        const int incl = lane_scan_i(n_lane);
+        const int pre_lane = pre + incl - n_lane;
+        int sel = -1;
+        if (b < 0) {
+            const unsigned long long m = __ballot(n_lane > 0 && pre_lane <= j && j < pre_lane + n_lane);
+            if (m != 0) sel = __builtin_ctzll(m);
+        } else if (b / kWave == r) {
+            sel = b - r * kWave;
+        }
+        if (sel >= 0) {
+            sp.b = r * kWave + sel;
+            sp.n_b = __shfl(n_lane, sel, kWave);
+            sp.rec0 = __shfl(pre_lane, sel, kWave);
+            sp.g.lo = __shfl(g.lo, sel, kWave);
+            sp.g.n_kv = __shfl(g.n_kv, sel, kWave);
+            sp.g.t0 = __shfl(g.t0, sel, kWave);
+            sp.g.n_tiles = __shfl(g.n_tiles, sel, kWave);
+            sp.split = j - sp.rec0;
             return true;
         }
-        pre += nb;
+        pre += __shfl(incl, kWave - 1, kWave);
     }
     return false;
 }

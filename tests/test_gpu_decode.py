@@ -218,10 +218,10 @@ def test_decode_q8_window_and_placement(gpu, oracle_mod):
 
 
 @pytest.mark.parametrize("kv_type", [1, 8])
-@pytest.mark.parametrize("B", [2, 64, 65, 100])
+@pytest.mark.parametrize("B", [2, 64, 65, 100, 256, 333])
 def test_decode_split_plan_batches(gpu, oracle_mod, kv_type, B):
     # the split plan deals each kv head's row of workgroups out by sequence
-    # length: a lane per sequence up to 64 sequences, a sequential walk above;
+    # length: a lane per sequence up to 64 sequences, rounds of 64 above;
     # lengths span empty, one token, one tile and a few thousand positions,
     # some with a window start, and max_seq_len overstates the longest span
     rng = np.random.default_rng(100 + B + kv_type)
