@@ -96,10 +96,34 @@ def _lib_mod():
     return _lib
 
 
+def time_split_launches(torch, lib, args, reps: int):
+    """Mean and median duration (us) of one split-K pass launch: the launches
+    of all layers back to back between two events on the launching stream,
+    queued behind a backlog so host launch cost stays off the GPU clock;
+    `reps` such batches.  (Events around every single launch would add the
+    command processor's marker latency, about 1.7 us, to each; the profiler's
+    per-dispatch durations sit a few percent above this back-to-back figure.)"""
+    from strataflow_amd import _lib
+    n = len(args)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    calibrate_backlog(torch)
+    torch.cuda.synchronize()
+    gpu_backlog(torch, 0.05 * n * reps + 5)
+    for a, b in evs:
+        a.record()
+        for x in args:
+            _lib.check(lib.sfa_attn_decode_split(*x), "sfa_attn_decode_split")
+        b.record()
+    torch.cuda.synchronize()
+    d = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3 / n
+    return float(np.mean(d)), float(np.median(d))
+
+
 def time_decode(torch, kv, t_pt, q, seq_len, ctx, steps, warmup):
     """Step timing: the 32-layer loop captured once as a HIP graph and
-    replayed `steps` times between two events.  Kernel timing: the split-K
-    passes of the 32 layers back to back between two events."""
+    replayed `steps` times between two events.  Kernel timing: every split-K
+    pass launch of the 32 layers between its own two events."""
     B = int(seq_len.numel())
     out = torch.empty((N_LAYER, B, HQ * HD), device=q.device)
     kv.workspace(B, ctx)
@@ -133,31 +157,31 @@ def time_decode(torch, kv, t_pt, q, seq_len, ctx, steps, warmup):
     torch.cuda.synchronize()
     ms_eager = t0.elapsed_time(t1) / steps
 
-    # split-K kernel time: the split passes of all layers back to back between
-    # two events (queued behind a backlog, so host launch cost is hidden),
-    # divided by the launch count; repeated `steps` times
-    calibrate_backlog(torch)
     lib = _lib_mod().load()
     ws = kv.workspace(B, ctx)
     stream = torch.cuda.current_stream().cuda_stream
     args = [(ctypes.byref(kv.desc(layer)), q[layer].data_ptr(), out[layer].data_ptr(), t_pt.data_ptr(),
              int(t_pt.shape[1]), seq_len.data_ptr(), None, B, int(ctx), float(kv.scale), ws.data_ptr(),
              ws.numel(), stream) for layer in range(N_LAYER)]
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
-    torch.cuda.synchronize()
-    gpu_backlog(torch, 0.05 * N_LAYER * steps + 5)
-    for a, b in evs:
-        a.record()
-        for layer in range(N_LAYER):
-            lib.sfa_attn_decode_split(*args[layer])
-        b.record()
-    torch.cuda.synchronize()
-    durs = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3 / N_LAYER  # us per launch
+    k_mean, k_med = time_split_launches(torch, lib, args, max(steps // 2, 4))
     for layer in range(N_LAYER):  # leave complete outputs behind
         kv.decode(layer, q[layer], t_pt, seq_len, ctx, out=out[layer])
     torch.cuda.synchronize()
-    return ms_per_step, ms_eager, float(np.mean(durs)), float(np.median(durs)), out
+    return ms_per_step, ms_eager, k_mean, k_med, out
+
+
+def hbm_roofline(alg_bytes: int, k_mean_us: float, node_us: float, kernel: str, key: str) -> dict:
+    """The split-K kernel's HBM roofline (algorithmic bytes over its mean
+    launch duration) with the node's (split + merge + launch gaps) beside it."""
+    ach = alg_bytes / (k_mean_us * 1e-6) / 1e9
+    node = alg_bytes / (node_us * 1e-6) / 1e9
+    return with_traffic({
+        "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
+        "kernel_us_mean": round(k_mean_us, 3), "bytes_per_launch": alg_bytes,
+        "node": {"us": round(node_us, 3), "achieved": round(node, 1), "frac": round(node / HBM_PEAK_GBS, 4),
+                 "what": "the whole attention node per layer (split pass, merge pass, launch gaps) "
+                         "from the graph-replayed step"}}, key)
 
 
 def load_traffic() -> dict:
@@ -183,15 +207,28 @@ def with_traffic(roofline: dict, key: str) -> dict:
 KV_NAMES = {0: "f32", 1: "f16", 8: "Q8_0"}
 
 
-def decode_leg(torch, key, lens, kv_type, steps, warmup, seed):
+def decode_cpu_leg(kv, pt, q_layer0, lens, gpu_out0, budget_s: float) -> dict:
+    """The oracle on layer 0 of a decode workload (all sequences of the step):
+    the same seeded bytes, the same Q."""
+    from oracle import oracle
+    host = host_kv_from_device(kv, 0)
+    q = q_layer0.cpu().numpy().reshape(len(lens), HQ, HD)
+    sl = np.asarray(lens, np.int32)
+    return cpu_leg(lambda nt: host.attention(q, HQ, pt, sl, n_threads=nt, mode=oracle.GGML),
+                   "us/layer-step", 1e6,
+                   f"layer 0 of the same workload ({len(lens)} sequence(s), "
+                   f"{int(sl.sum())} positions), ggml-semantics oracle", budget_s,
+                   gpu_out=gpu_out0)
+
+
+def decode_leg(torch, key, lens, kv_type, steps, warmup, seed, cpu_budget_s: float = 0.0):
     """One decode workload: lens (one entry per sequence), f32, f16 or Q8_0."""
     kv, pt, t_pt, q, seq_len = build_decode_workload(torch, lens, seed, kv_type=kv_type)
     mx = int(max(lens))
-    ms, _, k_mean, _, _ = time_decode(torch, kv, t_pt, q, seq_len, mx, steps, warmup)
+    ms, _, k_mean, _, out = time_decode(torch, kv, t_pt, q, seq_len, mx, steps, warmup)
     row = {0: HD * 4, 1: HD * 2, 8: HD // 32 * 34}[kv_type]
     alg = 2 * sum(lens) * HKV * row + len(lens) * HQ * HD * 4 * 2
     us_layer = ms * 1e3 / N_LAYER
-    ach = alg / (k_mean * 1e-6) / 1e9
     # Q8_0 batches of two or more with >= 1024 tiles in all run the column layout
     cols = kv_type == 8 and len(lens) >= 2 and len(lens) * ((mx + 31) // 32) >= 1024
     kname = {0: "decode_f32_kernel<128,4>", 1: "decode_f16_kernel<128,4>",
@@ -203,25 +240,25 @@ def decode_leg(torch, key, lens, kv_type, steps, warmup, seed):
         "us_per_layer_step": round(us_layer, 3),
         "us_per_layer_token": round(us_layer / len(lens), 3),
         "tokens_per_s": round(len(lens) * 1e3 / ms, 1),
-        "roofline": with_traffic({
-            "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": f"{kname} (split-K pass)", "kernel_us_mean": round(k_mean, 3),
-            "bytes_per_launch": alg}, key),
+        "roofline": hbm_roofline(alg, k_mean, us_layer, f"{kname} (split-K pass)", key),
     }
-    del kv, q
+    if cpu_budget_s > 0:
+        res["cpu_baseline"] = decode_cpu_leg(kv, pt, q[0], lens, out[0].cpu().numpy(), cpu_budget_s)
+    del kv, q, out
     torch.cuda.empty_cache()
     return res
 
 
-def q8_bench(torch, steps, warmup, seed):
+def q8_bench(torch, steps, warmup, seed, cpu_budget_s: float = 0.0):
     """Q8_0 KV decode: (a) batch 1 at context 32768; (b) batch 8 with lengths
     uniform in [8192, 32768] sharing one page pool; and the 2048-on-2048 chunked
     prefill over a Q8_0 cache."""
     lens_b8 = [int(x) for x in np.random.default_rng(seed).integers(8192, 32769, 8)]
     return {
-        "ctx32k_b1": decode_leg(torch, "decode_q8_0_ctx32k_b1", [32768], 8, steps, warmup, seed),
-        "b8_varlen_8k_32k": decode_leg(torch, "decode_q8_0_b8", lens_b8, 8, steps, warmup, seed),
+        "ctx32k_b1": decode_leg(torch, "decode_q8_0_ctx32k_b1", [32768], 8, steps, warmup, seed,
+                                cpu_budget_s),
+        "b8_varlen_8k_32k": decode_leg(torch, "decode_q8_0_b8", lens_b8, 8, steps, warmup, seed,
+                                       cpu_budget_s),
         "prefill_2048_on_2048": prefill_bench(torch, max(steps // 3, 3), 2, seed + 1, kv_type=8),
     }
 
@@ -247,9 +284,9 @@ def copy_ceiling(torch) -> dict:
             "what": "2 GiB device copy (read + write bytes), torch"}
 
 
-def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1):
+def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1, cpu_budget_s: float = 0.0):
     """Chunked causal prefill: 2048 tokens at positions 2048..4095 over a
-    4096-position paged f16 (or f32) cache, 8 layers with distinct caches."""
+    4096-position paged f16 (Q8_0, f32) cache, 8 layers with distinct caches."""
     from strataflow_amd import synth
     from strataflow_amd.paged_kv import PagedKV
     dev = torch.device("cuda:0")
@@ -298,7 +335,28 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1):
     # f32: the f32 MFMA peak; Q8_0 (int8 QK, f16 PV): the f16 peak, the slower of its two
     peak = MFMA_F32_PEAK_TFLOPS if kv_type == 0 else MFMA_F16_PEAK_TFLOPS
     name = KV_NAMES[kv_type]
-    return {
+    cpu = None
+    if cpu_budget_s > 0:
+        from oracle import oracle
+        out0 = kv.prefill(0, qs[0], pt, n_cached).cpu().numpy()
+        host = host_kv_from_device(kv, 0)
+        q0 = qs[0].cpu().numpy()
+        pt_h = pt.cpu().numpy()[None]
+        nkv = np.array([n_kv], np.int32)
+        one = kv_head_sample(host, 1)
+        q_one = np.ascontiguousarray(q0[:, : HQ // HKV])
+        cpu = cpu_leg(lambda nt: host.attention(q0[None], HQ, pt_h, nkv, T=T, n_threads=nt,
+                                                mode=oracle.GGML),
+                      "us/layer-chunk", 1e6,
+                      "layer 0 of the same workload (the whole 2048-token chunk, all 32 heads), "
+                      "ggml-semantics oracle with the causal mask", cpu_budget_s,
+                      run_1t=lambda nt: one.attention(q_one[None], HQ // HKV, pt_h, nkv, T=T, n_threads=nt,
+                                                      mode=oracle.GGML),
+                      scale_1t=1e6 * HKV,
+                      sample_1t="kv head 0 of layer 0 (its 4 query heads, the whole chunk), times 8 "
+                                "kv heads; ggml-semantics oracle with the causal mask",
+                      gpu_out=out0)
+    res = {
         "workload": f"causal prefill {name} KV, 2048-token chunk on 2048 cached, Mixtral GQA 32q/8kv hd128",
         "us_per_layer_chunk": round(us, 2),
         "us_per_layer_token": round(us / T, 5),
@@ -312,6 +370,11 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1):
                                   8: "prefill_q8_0_2048_on_2048"}[kv_type]),
         "flop_per_layer_chunk": flops,
     }
+    if cpu is not None:
+        res["cpu_baseline"] = cpu
+    del kv, qs, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def f32_bench(torch, steps: int, warmup: int, seed: int):
@@ -323,21 +386,48 @@ def f32_bench(torch, steps: int, warmup: int, seed: int):
     }
 
 
-def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 4):
+HOST_LINK_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction (the GPU reading host memory)
+
+
+def window_cpu_leg(B: int, hist: int, W: int, lossless: bool, budget_s: float, seed: int) -> dict:
+    """The oracle on one layer-step of the window workload's shape: B sequences
+    of `hist` positions (f16), attending all of them (lossless) or the last W.
+    The cache holds seeded f16 values of the same shape (the oracle's cost does
+    not depend on them); parity of this workload is the tests' business."""
+    from oracle import oracle
+    n_pages = B * hist // PAGE
+    host = oracle.HostPagedKv(HKV, HD, PAGE, oracle.KV_F16, n_pages)
+    rng = np.random.default_rng(seed)
+    tile = rng.standard_normal((8, host.page_bytes // 2)).astype(np.float16).view(np.uint8)
+    host.k[:] = np.tile(tile, (n_pages // 8, 1))
+    host.v[:] = np.tile(tile[::-1], (n_pages // 8, 1))
+    pt = rng.permutation(n_pages).astype(np.int32).reshape(B, -1)
+    q = rng.standard_normal((B, HQ, HD)).astype(np.float32)
+    sl = np.full(B, hist, np.int32)
+    lo = None if lossless else sl - W
+    what = (f"one layer-step: {B} sequences of {hist} positions, every position attended (lossless)"
+            if lossless else f"one layer-step: {B} sequences, the last {W} of {hist} positions attended")
+    return cpu_leg(lambda nt: host.attention(q, HQ, pt, sl, lo, n_threads=nt, mode=oracle.GGML),
+                   "us/layer-step", 1e6, what + ", ggml-semantics oracle, seeded f16 values", budget_s)
+
+
+def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 8, cpu_budget_s: float = 0.0):
     """KV-window decode under paging pressure: 4 sequences with 65536-token
     histories, a 4096-position window, the device pool sized to the window
     (4 x 17 pages per layer), pages evicted and reused by the host page
-    manager every 256 steps of a sequence.  (a) the opt-in sliding window over
-    all 32 layers for `steps` decode steps; (b) the reference's lossless
-    semantics (every position attended, the 61440 evicted positions read from
-    the host-pinned cold pool in place) on one layer."""
-    from strataflow_amd import synth
+    manager every 256 steps of a sequence, all 32 layers.  (a) the opt-in
+    sliding window for `steps` decode steps; (b) the reference's lossless
+    semantics (every position attended, the evicted positions read from the
+    host-pinned cold pool in place) for `lossless_steps` steps."""
+    from strataflow_amd import _lib, synth
     from strataflow_amd.pager import SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, KvPager
     dev = torch.device("cuda:0")
     B, hist, W = 4, 65536, 4096
+    pos_bytes = HKV * HD * 2 * 2  # K and V of one position, all kv heads (f16)
     res = {}
-    for name, attend, n_layer, n_steps in (("sliding_window", SFA_ATTEND_WINDOW, N_LAYER, steps),
-                                           ("lossless", SFA_ATTEND_LOSSLESS, 1, lossless_steps)):
+    for name, attend, n_steps in (("sliding_window", SFA_ATTEND_WINDOW, steps),
+                                  ("lossless", SFA_ATTEND_LOSSLESS, lossless_steps)):
+        n_layer = N_LAYER
         pager = KvPager(n_layer=n_layer, n_head=HQ, n_head_kv=HKV, head_dim=HD, kv_type=SFA_KV_F16,
                         page_size=PAGE, n_seq=B, n_ctx=hist + n_steps, window=W, attend=attend,
                         seed=seed)
@@ -394,32 +484,78 @@ def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 4):
             graph.replay()
         t1.record()
         torch.cuda.synchronize()
-        n_steps -= 1
-        us = t0.elapsed_time(t1) * 1e3 / (n_steps * n_layer)
+        timed = n_steps - 1
+        us = t0.elapsed_time(t1) * 1e3 / (timed * n_layer)
+
+        # bytes of the last step: resident positions from HBM, cold ones over
+        # the host link (every attended position once, K and V)
+        pt_h, used = pager.tables()
+        hbm = link = 0
+        for b in range(B):
+            n = int(used[b])
+            lo = n - W if attend == SFA_ATTEND_WINDOW else 0
+            for lp in range(lo // PAGE, (n - 1) // PAGE + 1):
+                cnt = min(n, (lp + 1) * PAGE) - max(lo, lp * PAGE)
+                if pt_h[b, lp] >= 0:
+                    hbm += cnt * pos_bytes
+                elif pt_h[b, lp] <= -2:
+                    link += cnt * pos_bytes
+        qo = B * HQ * HD * 4 * 2
+        # the split pass alone, over the pager's pools and tables, per launch
+        lib = _lib.load()
+        d_pt, d_sl, d_lo = pager.device_tables()
+        d0 = pager.desc(0)
+        ws_n = lib.sfa_decode_workspace_bytes(ctypes.byref(d0), B, pager.max_span)
+        ws = torch.empty(ws_n, dtype=torch.uint8, device=dev)
+        descs = [pager.desc(layer) for layer in range(n_layer)]
+        stream = torch.cuda.current_stream().cuda_stream
+        args = [(ctypes.byref(descs[layer]), qb[layer].data_ptr(), out[layer].data_ptr(), d_pt,
+                 pager.max_pages, d_sl, d_lo if attend == SFA_ATTEND_WINDOW else None, B,
+                 pager.max_span, 1.0 / math.sqrt(HD), ws.data_ptr(), ws_n, stream)
+                for layer in range(n_layer)]
+        k_mean, _ = time_split_launches(torch, lib, args, 4 if attend == SFA_ATTEND_WINDOW else 1)
         st = pager.stats()
-        hbm = B * W * HKV * HD * 2 * 2
         entry = {
             "workload": f"decode-attn f16 KV, Mixtral GQA 32q/8kv hd128, B={B}, history {hist}, "
                         f"window {W}, device pool {B * (W // PAGE + 1)} pages/layer, "
-                        f"{n_steps} consecutive steps, {n_layer} layer(s)",
+                        f"{timed} consecutive timed steps (+1 warm), {n_layer} layers",
             "semantics": ("sliding window: attends the last 4096 positions (opt-in kv_lo)"
                           if attend == SFA_ATTEND_WINDOW else
                           "lossless (reference): attends every position; evicted pages read "
                           "from the host-pinned cold pool"),
+            "steps": timed,
             "us_per_layer_step": round(us, 3),
             "us_per_layer_token": round(us / B, 3),
+            "tokens_per_s": round(B * 1e6 / (us * n_layer), 1),
             "includes": "paging (plan + table update), KV append, split-K decode and merge",
             "pages_evicted": st["pages_evicted"], "pages_dropped": st["pages_dropped"],
-            "hbm_bytes_per_layer_step": hbm,
-            "hbm_gbs": round(hbm / (us * 1e-6) / 1e9, 1),
+            "hbm_bytes_per_layer_step": hbm + qo,
+            "host_link_bytes_per_layer_step": link,
         }
-        if attend == SFA_ATTEND_LOSSLESS:
-            cold = sum(hist + s - W for s in range(n_steps)) // n_steps * B * HKV * HD * 2 * 2
-            entry["host_link_bytes_per_layer_step"] = cold
-            entry["host_link_gbs"] = round(cold / (us * 1e-6) / 1e9, 1)
+        kname = "decode_f16_kernel<128,4> (split-K pass)"
+        if attend == SFA_ATTEND_WINDOW:
+            entry["roofline"] = hbm_roofline(hbm + qo, k_mean, us, kname, "window_sliding")
+        else:
+            ach = link / (k_mean * 1e-6) / 1e9
+            node = link / (us * 1e-6) / 1e9
+            entry["roofline"] = with_traffic({
+                "bound": "host_link", "achieved": round(ach, 1), "peak": HOST_LINK_PEAK_GBS,
+                "unit": "GB/s", "frac": round(ach / HOST_LINK_PEAK_GBS, 4), "traffic": None,
+                "kernel": kname, "kernel_us_mean": round(k_mean, 3), "bytes_per_launch": link,
+                "what": "cold-page bytes read over the host link (PCIe 5.0 x16, 64 GB/s a direction)",
+                "node": {"us": round(us, 3), "achieved": round(node, 1),
+                         "frac": round(node / HOST_LINK_PEAK_GBS, 4)}}, "window_lossless")
+            hb = (hbm + qo) / (k_mean * 1e-6) / 1e9
+            entry["roofline_hbm"] = {"bound": "hbm", "achieved": round(hb, 1), "peak": HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(hb / HBM_PEAK_GBS, 4),
+                                     "bytes_per_launch": hbm + qo,
+                                     "what": "window-resident bytes read from HBM by the same launches"}
+        if cpu_budget_s > 0:
+            entry["cpu_baseline"] = window_cpu_leg(B, hist, W, attend == SFA_ATTEND_LOSSLESS,
+                                                   cpu_budget_s, seed)
         res[name] = entry
         pager.close()
-        del qs, ks, vs
+        del qs, ks, vs, graph
         torch.cuda.empty_cache()
     return res
 
@@ -511,28 +647,102 @@ def rope_bench(torch, steps: int, seed: int):
     return res
 
 
-def cpu_baseline(kv, pt, q_layer0, ctx, budget_s=12.0):
-    """The oracle (ggml semantics, the reference's op sequence with its three
-    history copies) on the host cores, layer 0 of the same workload."""
-    import torch
+# ---- CPU baseline: the oracle (ggml semantics) on the host cores ------------------
+#
+# The oracle restates the reference's op sequence (engine.cpp:1751-1761) with its
+# cost structure: the gather into the column layout, the two cont(permute) copies
+# and the cont(transpose) of V, then mul_mat -> soft_max_ext -> mul_mat.  It runs
+# at one thread (the reference's determinism setting, engine.cpp:1013-1019) and
+# at every host thread the process may use; each leg states its sample.
+
+def host_info() -> dict:
+    """CPU model, logical CPUs, the CPUs this process may run on and the
+    thread count the CPU legs use (the affinity set, capped by OMP_NUM_THREADS
+    when the environment sets it: the GPU host allots a share of its cores to
+    each GPU)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(aff, int(omp)) if omp.isdigit() and int(omp) > 0 else aff
+    model, phys = "", None
+    try:
+        with open("/proc/cpuinfo") as f:
+            info = f.read()
+        for line in info.splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+        cores = {(blk.split("physical id")[1].split(":")[1].split()[0],
+                  blk.split("core id")[1].split(":")[1].split()[0])
+                 for blk in info.split("\n\n") if "core id" in blk and "physical id" in blk}
+        phys = len(cores) or None
+    except (OSError, IndexError):
+        pass
+    return {"model": model, "nproc": os.cpu_count(), "physical_cores": phys, "affinity_cpus": aff,
+            "omp_num_threads": omp or None, "threads_used": threads}
+
+
+def cpu_median(fn, budget_s: float, max_calls: int = 200):
+    """Median seconds of fn() over about budget_s (a call slower than a third
+    of the budget is timed once, without a warm-up call)."""
+    t0 = time.perf_counter()
+    out = fn()
+    first = time.perf_counter() - t0
+    if first > budget_s / 3:
+        return first, 1, out
+    ts = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s and len(ts) < max_calls:
+        t0 = time.perf_counter()
+        out = fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts), out
+
+
+def host_kv_from_device(kv, layer: int):
+    """The oracle's host pools holding a copy of one layer of a PagedKV."""
     from oracle import oracle
-    host = oracle.HostPagedKv(HKV, HD, PAGE, oracle.KV_F16, kv.n_pages)
-    host.k[:] = kv.k[0].cpu().numpy()
-    host.v[:] = kv.v[0].cpu().numpy()
-    q = q_layer0.cpu().numpy().reshape(1, HQ, HD)
-    sl = np.array([ctx], np.int32)
-    threads = min(os.cpu_count() or 1, 16)
-    res = {}
-    for nt in (threads, 1):
-        host.attention(q, HQ, pt, sl, n_threads=nt)  # warm
-        ts = []
-        t_start = time.perf_counter()
-        while time.perf_counter() - t_start < budget_s / 2 and len(ts) < 200:
-            t0 = time.perf_counter()
-            out = host.attention(q, HQ, pt, sl, n_threads=nt)
-            ts.append(time.perf_counter() - t0)
-        res[nt] = (float(np.median(ts)) * 1e6, len(ts), out)
-    return threads, res
+    host = oracle.HostPagedKv(kv.n_head_kv, kv.head_dim, kv.page_size, kv.kv_type, kv.n_pages)
+    host.k[:] = kv.k[layer].cpu().numpy()
+    host.v[:] = kv.v[layer].cpu().numpy()
+    return host
+
+
+def kv_head_sample(host, n_keep: int = 1):
+    """The first n_keep kv heads of a host cache as a cache of their own (the
+    oracle's work scales linearly with kv heads)."""
+    from oracle import oracle
+    Hkv, rb = host.n_head_kv, host.page_bytes // (host.page_size * host.n_head_kv)
+    small = oracle.HostPagedKv(n_keep, host.head_dim, host.page_size, host.kv_type, host.n_pages)
+    for src, dst in ((host.k, small.k), (host.v, small.v)):
+        dst[:] = src.reshape(src.shape[0], host.page_size, Hkv, rb)[:, :, :n_keep].reshape(dst.shape)
+    return small
+
+
+def parity(gpu_out, ref) -> dict:
+    g = np.asarray(gpu_out, np.float64).reshape(-1)
+    r = np.asarray(ref, np.float64).reshape(-1)
+    return {"max_abs": float(np.max(np.abs(g - r))),
+            "rel_l2": float(np.linalg.norm(g - r) / np.linalg.norm(r))}
+
+
+def cpu_leg(run, unit: str, scale_us: float, sample: str, budget_s: float, run_1t=None,
+            scale_1t: float | None = None, sample_1t: str | None = None, gpu_out=None) -> dict:
+    """The oracle at every allotted thread and at one thread.  run(n_threads)
+    performs one sampled call; scale_us turns its seconds into the leg's unit.
+    run_1t / scale_1t / sample_1t give a smaller one-thread sample (the same
+    work per unit, fewer units) when the full one would take too long."""
+    hi = host_info()
+    nt = hi["threads_used"]
+    s_all, n_all, out = cpu_median(lambda: run(nt), budget_s)
+    r1 = run_1t or run
+    s_one, n_one, _ = cpu_median(lambda: r1(1), budget_s)
+    res = {"value": round(s_all * scale_us, 1), "unit": unit, "cores": nt, "kind": "port",
+           "sample": f"{sample}; median of {n_all} call(s)",
+           "value_1_thread": round(s_one * (scale_1t if scale_1t is not None else scale_us), 1),
+           "sample_1_thread": f"{sample_1t or sample}; median of {n_one} call(s)"}
+    if gpu_out is not None:
+        res["parity_vs_gpu"] = parity(gpu_out, out)
+    return res
 
 
 def main():
@@ -542,7 +752,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--cpu-budget", type=float, default=4.0, metavar="S",
+                    help="seconds of timed CPU work per thread count and CPU leg")
+    ap.add_argument("--window-lossless-steps", type=int, default=8, metavar="N",
+                    help="decode steps of the lossless window leg (N-1 timed)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 decode legs")
     ap.add_argument("--no-window", action="store_true", help="skip the KV-window paging legs")
@@ -592,18 +806,21 @@ def main():
         elif args.only == "f32":
             r = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
         else:
-            r = window_bench(torch, args.seed + 3)
+            r = window_bench(torch, args.seed + 3, lossless_steps=args.window_lossless_steps)
         print(json.dumps({args.only: r}))
         return
 
     ctx = args.ctx
+    cpu_s = 0.0 if args.no_cpu else args.cpu_budget
     kv, pt, t_pt, q, seq_len = build_decode_workload(torch, ctx, args.seed)
     ms_step, ms_eager, k_mean, k_med, out = time_decode(torch, kv, t_pt, q, seq_len, ctx, args.steps,
                                                         args.warmup)
     us_layer = ms_step * 1e3 / N_LAYER
     kv_bytes = 2 * ctx * HKV * HD * 2
     alg_bytes = kv_bytes + HQ * HD * 4 * 2  # K + V + Q + O, each once
-    achieved = alg_bytes / (k_mean * 1e-6) / 1e9
+    roof = hbm_roofline(alg_bytes, k_mean, us_layer, "decode_f16_kernel<128,4> (split-K pass)",
+                        "decode_f16_ctx4096")
+    roof["kernel_us_median"] = round(k_med, 3)
 
     result = {
         "metric": METRIC,
@@ -627,42 +844,31 @@ def main():
         "timing": "32-layer step captured as a HIP graph, replayed; eager (per-call host "
                   "launch) step also reported",
         "ms_per_step_eager": round(ms_eager, 4),
-        "roofline": with_traffic({
-            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "decode_f16_kernel<128,4> (split-K pass)", "kernel_us_mean": round(k_mean, 3),
-            "kernel_us_median": round(k_med, 3), "bytes_per_launch": alg_bytes,
-        }, "decode_f16_ctx4096"),
+        "roofline": roof,
     }
+    if cpu_s > 0:
+        cb = decode_cpu_leg(kv, pt, q[0], [ctx], out[0].cpu().numpy(), cpu_s)
+        cb["unit"] = "us/layer-token"
+        result["cpu_baseline"] = cb
+        result["host"] = host_info()
+    del kv, q, out
+    torch.cuda.empty_cache()
     if not args.no_32k:
         result["f16_ctx32k"] = decode_leg(torch, "decode_f16_ctx32k", [32768], 1,
                                           max(args.steps // 4, 5), 3, args.seed + 4)
     if not args.no_prefill:
-        result["prefill"] = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1)
+        result["prefill"] = prefill_bench(torch, max(args.steps // 10, 3), 2, args.seed + 1,
+                                          cpu_budget_s=cpu_s)
     if not args.no_q8:
-        result["q8_0"] = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2)
+        result["q8_0"] = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2, cpu_budget_s=cpu_s)
     if not args.no_window:
-        result["window"] = window_bench(torch, args.seed + 3)
+        result["window"] = window_bench(torch, args.seed + 3, lossless_steps=args.window_lossless_steps,
+                                        cpu_budget_s=cpu_s)
     if not args.no_rope:
         result["rope_append"] = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
     if not args.no_f32:
         result["f32"] = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
     result["hbm_copy_ceiling"] = copy_ceiling(torch)
-    if not args.no_cpu:
-        threads, res = cpu_baseline(kv, pt, q[0], ctx)
-        us_all, n_all, cpu_out = res[threads]
-        us_one, n_one, _ = res[1]
-        gpu0 = out[0].cpu().numpy().reshape(-1).astype(np.float64)
-        ref = cpu_out.reshape(-1).astype(np.float64)
-        ma = float(np.max(np.abs(gpu0 - ref)))
-        rl = float(np.linalg.norm(gpu0 - ref) / np.linalg.norm(ref))
-        result["cpu_baseline"] = {
-            "value": round(us_all, 1), "unit": "us/layer-token", "cores": threads, "kind": "port",
-            "sample": f"layer 0 of the same workload (ctx {ctx}), ggml-semantics oracle, "
-                      f"median of {n_all} calls",
-            "value_1_thread": round(us_one, 1),
-            "parity_vs_gpu": {"max_abs": ma, "rel_l2": rl},
-        }
     print(json.dumps(result))
 
 
