@@ -377,6 +377,70 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1, c
     return res
 
 
+def decode_wo_bench(torch, steps: int, warmup: int, seed: int):
+    """The decode node with its consumer fused in (sfa_attn_decode_wo):
+    y = wo @ attn + residual, wo f16 [4096, 4096] per layer (the Mixtral
+    attn_output.weight shape), B=1, context 4096, 32 layers with distinct caches
+    and weights, graph-replayed.  Beside it the unfused chain: the decode node,
+    then the projection and the residual add as torch ops (f16 GEMV, casts, add)."""
+    n_embd = HQ * HD
+    kv, pt, t_pt, q, seq_len = build_decode_workload(torch, 4096, seed)
+    dev = q.device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    wo = [(torch.randn((n_embd, HQ * HD), device=dev, generator=gen) / math.sqrt(HQ * HD)).half()
+          for _ in range(N_LAYER)]
+    x = torch.randn((N_LAYER, 1, n_embd), device=dev, generator=gen)
+    y = torch.empty_like(x)
+    attn = torch.empty((N_LAYER, 1, HQ * HD), device=dev)
+
+    def fused():
+        for layer in range(N_LAYER):
+            kv.decode_wo(layer, q[layer], t_pt, seq_len, 4096, wo[layer], x[layer], y=y[layer])
+
+    def unfused():
+        for layer in range(N_LAYER):
+            kv.decode(layer, q[layer], t_pt, seq_len, 4096, out=attn[layer])
+            y[layer] = torch.nn.functional.linear(attn[layer].half(), wo[layer]).float() + x[layer]
+
+    res = {}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) * 1e3 / (steps * N_LAYER)
+        del g
+    alg = 2 * 4096 * HKV * HD * 2 + HQ * HD * 4 + n_embd * HQ * HD * 2 + 2 * n_embd * 4
+    ach = alg / (res["fused"] * 1e-6) / 1e9
+    out = {
+        "workload": "decode-attn f16 KV + output projection (wo f16 [4096, 4096]) + residual, Mixtral GQA "
+                    "32q/8kv hd128, B=1, context 4096, 32 layers with distinct caches and weights",
+        "us_per_layer_token": round(res["fused"], 3),
+        "us_per_layer_token_unfused": round(res["unfused"], 3),
+        "unfused": "sfa_attn_decode, then torch f16 linear + cast + residual add",
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "split-K pass + merge_wo_kernel<128,4,f16> (the node, graph-replayed)",
+                     "bytes_per_launch": alg,
+                     "what": "K + V + Q + wo + residual + y once, over the node's time"},
+    }
+    del kv, q, wo
+    torch.cuda.empty_cache()
+    return out
+
+
 def f32_bench(torch, steps: int, warmup: int, seed: int):
     """F32 KV, the reference's own cache type: decode at context 4096 (B=1,
     32 layers) and the 2048-on-2048 chunked prefill, both on f32 MFMA."""
@@ -763,7 +827,8 @@ def main():
     ap.add_argument("--no-32k", action="store_true", help="skip the f16 context-32768 decode leg")
     ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE + append leg")
     ap.add_argument("--no-f32", action="store_true", help="skip the F32-cache legs")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope", "f32"],
+    ap.add_argument("--no-wo", action="store_true", help="skip the fused output-projection leg")
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope", "f32", "wo"],
                     help="run one leg only and print its JSON (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
@@ -793,7 +858,7 @@ def main():
 
     if args.only == "decode4k":
         args.no_prefill = args.no_q8 = args.no_window = args.no_32k = args.no_cpu = args.no_rope = True
-        args.no_f32 = True
+        args.no_f32 = args.no_wo = True
     if args.only and args.only != "decode4k":
         if args.only == "decode32k":
             r = decode_leg(torch, "decode_f16_ctx32k", [32768], 1, max(args.steps // 4, 5), 3, args.seed + 4)
@@ -805,6 +870,8 @@ def main():
             r = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
         elif args.only == "f32":
             r = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
+        elif args.only == "wo":
+            r = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
         else:
             r = window_bench(torch, args.seed + 3, lossless_steps=args.window_lossless_steps)
         print(json.dumps({args.only: r}))
@@ -868,6 +935,8 @@ def main():
         result["rope_append"] = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
     if not args.no_f32:
         result["f32"] = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
+    if not args.no_wo:
+        result["decode_wo"] = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
     result["hbm_copy_ceiling"] = copy_ceiling(torch)
     print(json.dumps(result))
 

@@ -24,47 +24,9 @@
 // writes back a whole XCD L2).
 #include <mutex>
 
-#include "sfa_common.h"
+#include "sfa_decode.h"
 
 namespace sfa {
-
-struct DecodeParams {
-    const uint8_t *k_pages;
-    const uint8_t *v_pages;
-    const uint8_t *k_cold;
-    const uint8_t *v_cold;
-    int64_t page_bytes;
-    int n_pages;
-    int n_cold;
-    int page_size;
-    int n_head_kv;
-    int n_head;
-    int row_bytes;
-    int kv_type;
-    const float *q;
-    float *out;
-    const int32_t *page_table;
-    int max_pages;
-    const int32_t *seq_len;
-    const int32_t *kv_lo;
-    int n_seq;            // B
-    int split_row;        // workgroup slots per kv head (a multiple of 8)
-    int guess_splits;     // the host's guess of splits per sequence (all at max_seq_len)
-    int guess_tiles;      // and of its tiles; the device plan decides
-    int one_split;        // 1: no merge pass runs (one sequence, guessed one split)
-    int cols_waves;       // Q8_0: kv heads per column-layout workgroup, 0 = per-kv-head layout
-    float scale_log2;     // scale * log2(e)
-    float *part;          // [Hkv][split_row][G][HD + 4]: one (o, m, l) record per slot
-};
-
-constexpr int kDecodeWaves = 4;
-constexpr int kColsWaves = 8;    // most waves (kv heads) of a column-layout Q8_0 workgroup
-constexpr int kMaxSplits = 256;  // splits per (sequence, kv head)
-constexpr int kMaxPlanTiles = 1 << 30;  // bound on the tiles of one call (all sequences)
-constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold: P <= 2^8
-// merge kernel block: one thread per dim, at least one full wave
-template <int HD>
-constexpr int kMergeThreads = HD < 64 ? 64 : HD;
 
 // Head of MFMA output register i (rows 8(i/4) + 4hh + i%4, row m is head
 // m % g) for the Q8_0 kernel's S = Q * K^T: (4hh + i) % g, a compile-time
@@ -82,215 +44,6 @@ __device__ inline float head_val(const float (&arr)[G], int i, int hh) {
     }
 }
 
-// ---- split plan --------------------------------------------------------------
-// Each kv head owns a row of `split_row` workgroup slots (XCD = L % 8 and
-// split_row % 8 == 0, so every kv head of one slot shares an XCD and its L2:
-// Q8_0 rows of neighbouring kv heads share cache lines).  The slots are dealt
-// out to the sequences in proportion to their active tiles: with T the sum of
-// the sequences' tiles and Z the number of sequences with any, sequence b of
-// n_b tiles takes 1 + floor((split_row - Z) * n_b / T) consecutive slots (at
-// most one per kDecodeWaves tiles, at most kMaxSplits), so the shares never
-// exceed the row and a short sequence in a batch does not leave slots idle
-// that a long one could use.  Inside a sequence the tiles are spread evenly:
-// splits differ by at most one tile.  The plan is computed on the device from
-// seq_len / kv_lo (device arrays), identically by every workgroup and by the
-// merge pass; the host only guesses it (every sequence at max_seq_len, from
-// position 0) so the first tile can be fetched before seq_len arrives.
-
-// Tiles of a sequence: 32-aligned absolute position blocks [32t, 32t+32)
-// intersecting [lo, n_kv).
-struct SeqGeom {
-    int lo, n_kv, t0, n_tiles;
-};
-__host__ __device__ inline SeqGeom seq_geom(int n_kv_raw, int lo_raw, int cap) {
-    SeqGeom g;
-    g.n_kv = n_kv_raw > cap ? cap : n_kv_raw;
-    g.lo = lo_raw < 0 ? 0 : lo_raw;
-    if (g.n_kv <= g.lo) {
-        g.t0 = 0;
-        g.n_tiles = 0;
-    } else {
-        g.t0 = g.lo / kTile;
-        g.n_tiles = (g.n_kv + kTile - 1) / kTile - g.t0;
-    }
-    return g;
-}
-
-__host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
-__host__ inline long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
-
-// Splits of a sequence with n tiles, given `avail` slots to share beyond one
-// per non-empty sequence and T tiles in all (T >= n).
-__host__ __device__ inline int splits_of(int n, int avail, int T) {
-    if (n <= 0) return 0;
-    const unsigned long long prod = (unsigned long long)avail * (unsigned)n;
-    const int share = prod <= 0xffffffffull ? (int)((unsigned)prod / (unsigned)T)
-                                            : (int)(prod / (unsigned long long)T);
-    int s = 1 + share;
-    const int most = ceil_div(n, kDecodeWaves);
-    if (s > most) s = most;
-    if (s > kMaxSplits) s = kMaxSplits;
-    return s;
-}
-
-// Tiles [lo, hi) of split s of n_s splits over n tiles from t0: the first
-// n % n_s splits take one tile more.
-__host__ __device__ inline void split_tiles(int t0, int n, int n_s, int s, int &lo, int &hi) {
-    const int q = n / n_s, r = n - q * n_s;
-    lo = t0 + s * q + (s < r ? s : r);
-    hi = lo + q + (s < r ? 1 : 0);
-}
-
-// Wave-wide integer sum (every lane gets the result) and inclusive prefix
-// sum, on DPP: butterflies or shifts inside each 16-lane row, then the rows
-// combined (readlanes for the sum; row_bcast:15 / row_bcast:31 for the scan,
-// as the atomic-optimizer scan of the AMDGPU backend does).
-template <int CTRL>
-__device__ inline int dpp_i(int x) {
-    return __builtin_amdgcn_mov_dpp(x, CTRL, 0xf, 0xf, false);
-}
-template <int CTRL, int ROWS>
-__device__ inline int dpp_i0(int x) {  // source lanes outside the row read 0
-    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xf, true);
-}
-__device__ inline int lane_sum_i(int x) {
-    x += dpp_i<0xB1>(x);
-    x += dpp_i<0x4E>(x);
-    x += dpp_i<0x141>(x);
-    x += dpp_i<0x140>(x);
-    return (__builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16)) +
-           (__builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48));
-}
-__device__ inline int lane_scan_i(int x) {
-    x += dpp_i0<0x111, 0xf>(x);  // row_shr:1
-    x += dpp_i0<0x112, 0xf>(x);  // row_shr:2
-    x += dpp_i0<0x114, 0xf>(x);  // row_shr:4
-    x += dpp_i0<0x118, 0xf>(x);  // row_shr:8
-    x += dpp_i0<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
-    x += dpp_i0<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
-    return x;
-}
-
-// The plan as one slot or one sequence sees it.
-struct SlotPlan {
-    int b;       // sequence
-    int split;   // split index within the sequence
-    int n_b;     // splits of the sequence
-    int rec0;    // its first slot in the row
-    SeqGeom g;   // the sequence's tiles
-};
-
-// Per-lane raw inputs of the plan, issued early in a kernel: lane l holds
-// sequence l (2 <= B <= 64); for a single sequence every lane holds it.
-struct PlanRaw {
-    int n_kv, lo;
-};
-__device__ inline PlanRaw plan_load(const DecodeParams &p, int lane) {
-    PlanRaw r{0, 0};
-    if (p.n_seq == 1) {
-        r.n_kv = p.seq_len[0];
-        r.lo = p.kv_lo ? p.kv_lo[0] : 0;
-    } else if (p.n_seq <= kWave && lane < p.n_seq) {
-        r.n_kv = p.seq_len[lane];
-        r.lo = p.kv_lo ? p.kv_lo[lane] : 0;
-    }
-    return r;
-}
-
-// Sequence b = -1 asks for the owner of row slot j (false: the slot is idle);
-// b >= 0 asks for sequence b's splits and first slot (the merge pass).  Every
-// lane of the wave must be active.  2 <= B <= 64: lane l computes sequence l;
-// larger batches take ceil(B / 64) rounds of the same lane-parallel sums and
-// scans (lane l of round r holds sequence 64r + l).
-__device__ inline bool plan_lanes(const DecodeParams &p, const PlanRaw &raw, int j, int b, int lane, SlotPlan &sp) {
-    sp = SlotPlan{0, 0, 0, 0, SeqGeom{0, 0, 0, 0}};
-    const int cap = p.max_pages * p.page_size;
-    const int row = p.split_row;
-    if (p.n_seq == 1) {
-        sp.g = seq_geom(raw.n_kv, raw.lo, cap);
-        sp.b = 0;
-        sp.n_b = splits_of(sp.g.n_tiles, p.one_split ? 0 : row - 1, sp.g.n_tiles);
-        sp.rec0 = 0;
-        sp.split = b < 0 ? j : 0;
-        return b >= 0 || j < sp.n_b;
-    }
-    if (p.n_seq <= kWave) {
-        const SeqGeom g = lane < p.n_seq ? seq_geom(raw.n_kv, raw.lo, cap) : SeqGeom{0, 0, 0, 0};
-        const int T = lane_sum_i(g.n_tiles);
-        const int Z = __popcll(__ballot(g.n_tiles > 0));
-        const int n_lane = splits_of(g.n_tiles, row - Z, T);
-        const int pre_lane = lane_scan_i(n_lane) - n_lane;  // exclusive prefix over the lanes
-        if (b < 0) {
-            const unsigned long long m = __ballot(n_lane > 0 && pre_lane <= j && j < pre_lane + n_lane);
-            if (m == 0) return false;
-            b = __builtin_ctzll(m);
-        }
-        sp.b = b;
-        sp.n_b = __shfl(n_lane, b, kWave);
-        sp.rec0 = __shfl(pre_lane, b, kWave);
-        sp.g.lo = __shfl(g.lo, b, kWave);
-        sp.g.n_kv = __shfl(g.n_kv, b, kWave);
-        sp.g.t0 = __shfl(g.t0, b, kWave);
-        sp.g.n_tiles = __shfl(g.n_tiles, b, kWave);
-        sp.split = j - sp.rec0;
-        return true;
-    }
-    // more than 64 sequences: rounds of 64, lane l holding sequence 64r + l
-    // (coalesced loads); T and Z first, then the slot prefix round by round
-    const int rounds = (p.n_seq + kWave - 1) / kWave;
-    auto geom = [&](int r) -> SeqGeom {
-        const int bb = r * kWave + lane;
-        return bb < p.n_seq ? seq_geom(p.seq_len[bb], p.kv_lo ? p.kv_lo[bb] : 0, cap) : SeqGeom{0, 0, 0, 0};
-    };
-    int T = 0, Z = 0;
-    for (int r = 0; r < rounds; ++r) {
-        const SeqGeom g = geom(r);
-        T += lane_sum_i(g.n_tiles);
-        Z += __popcll(__ballot(g.n_tiles > 0));
-    }
-    int pre = 0;  // slots of the earlier rounds
-    for (int r = 0; r < rounds; ++r) {
-        const SeqGeom g = geom(r);
-        const int n_lane = splits_of(g.n_tiles, row - Z, T);
-        const int incl = lane_scan_i(n_lane);
-        const int pre_lane = pre + incl - n_lane;
-        int sel = -1;
-        if (b < 0) {
-            const unsigned long long m = __ballot(n_lane > 0 && pre_lane <= j && j < pre_lane + n_lane);
-            if (m != 0) sel = __builtin_ctzll(m);
-        } else if (b / kWave == r) {
-            sel = b - r * kWave;
-        }
-        if (sel >= 0) {
-            sp.b = r * kWave + sel;
-            sp.n_b = __shfl(n_lane, sel, kWave);
-            sp.rec0 = __shfl(pre_lane, sel, kWave);
-            sp.g.lo = __shfl(g.lo, sel, kWave);
-            sp.g.n_kv = __shfl(g.n_kv, sel, kWave);
-            sp.g.t0 = __shfl(g.t0, sel, kWave);
-            sp.g.n_tiles = __shfl(g.n_tiles, sel, kWave);
-            sp.split = j - sp.rec0;
-            return true;
-        }
-        pre += __shfl(incl, kWave - 1, kWave);
-    }
-    return false;
-}
-
-// The plan with every field wave-uniform (scalar registers), so the tile
-// bounds and the interior / edge tests derived from it are scalar branches.
-__device__ inline bool plan(const DecodeParams &p, const PlanRaw &raw, int j, int b, int lane, SlotPlan &sp) {
-    const bool ok = plan_lanes(p, raw, j, b, lane, sp);
-    sp.b = __builtin_amdgcn_readfirstlane(sp.b);
-    sp.split = __builtin_amdgcn_readfirstlane(sp.split);
-    sp.n_b = __builtin_amdgcn_readfirstlane(sp.n_b);
-    sp.rec0 = __builtin_amdgcn_readfirstlane(sp.rec0);
-    sp.g.lo = __builtin_amdgcn_readfirstlane(sp.g.lo);
-    sp.g.n_kv = __builtin_amdgcn_readfirstlane(sp.g.n_kv);
-    sp.g.t0 = __builtin_amdgcn_readfirstlane(sp.g.t0);
-    sp.g.n_tiles = __builtin_amdgcn_readfirstlane(sp.g.n_tiles);
-    return ok;
-}
 
 // Workgroup epilogue of a split: the four waves' (m, l, O^T) for the g heads
 // (MFMA column n < g is head n; register i of dim block d holds dim
@@ -1502,10 +1255,10 @@ static int launch_f16_g(const DecodeParams &p, int G, int B, int Hkv, int passes
     }
 }
 
-int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
-                  int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
-                  int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
-                  int passes, hipStream_t stream) {
+int decode_setup(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
+                 int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                 int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
+                 DecodeParams *out_p) {
     const int Hkv = kv->n_head_kv, HD = kv->head_dim, G = kv->n_head / kv->n_head_kv;
     if (B <= 0 || max_seq_len <= 0 || max_pages <= 0) return SFA_ERR_INVALID_ARGUMENT;
     // the split plan sums tile counts over the batch in 32-bit integers
@@ -1516,6 +1269,9 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
         return SFA_ERR_INVALID_ARGUMENT;
     const size_t need = decode_workspace_bytes(B, Hkv, G, HD, max_seq_len);
     if (workspace == nullptr || ws_bytes < need) return SFA_ERR_INVALID_ARGUMENT;
+    if (kv->kv_type != SFA_KV_F32 && kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0)
+        return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type == SFA_KV_Q8_0 && HD < 64) return SFA_ERR_UNSUPPORTED;
     const bool cols = use_cols(kv->kv_type, HD, G, B, max_seq_len, kv_lo != nullptr);
     const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, kv_lo != nullptr, cols);
 
@@ -1545,20 +1301,33 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     p.cols_waves = cols ? cols_waves_of(Hkv) : 0;
     p.scale_log2 = scale * 1.4426950408889634f;
     p.part = static_cast<float *>(workspace);
-
     p.kv_type = kv->kv_type;
-    if (kv->kv_type != SFA_KV_F32 && kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0)
-        return SFA_ERR_UNSUPPORTED;
-    if (kv->kv_type == SFA_KV_Q8_0 && HD < 64) return SFA_ERR_UNSUPPORTED;
+    *out_p = p;
+    return SFA_OK;
+}
+
+int decode_run(const DecodeParams &p, int HD, int passes, hipStream_t stream) {
+    const int G = p.n_head / p.n_head_kv;
     int rc;
     switch (HD) {
-    case 32: rc = launch_f16_g<32>(p, G, B, Hkv, passes, stream); break;
-    case 64: rc = launch_f16_g<64>(p, G, B, Hkv, passes, stream); break;
-    case 128: rc = launch_f16_g<128>(p, G, B, Hkv, passes, stream); break;
+    case 32: rc = launch_f16_g<32>(p, G, p.n_seq, p.n_head_kv, passes, stream); break;
+    case 64: rc = launch_f16_g<64>(p, G, p.n_seq, p.n_head_kv, passes, stream); break;
+    case 128: rc = launch_f16_g<128>(p, G, p.n_seq, p.n_head_kv, passes, stream); break;
     default: return SFA_ERR_UNSUPPORTED;
     }
     if (rc != SFA_OK) return rc;
     return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+}
+
+int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
+                  int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
+                  int32_t max_seq_len, float scale, void *workspace, size_t ws_bytes,
+                  int passes, hipStream_t stream) {
+    DecodeParams p;
+    const int rc = decode_setup(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
+                                workspace, ws_bytes, &p);
+    if (rc != SFA_OK) return rc;
+    return decode_run(p, kv->head_dim, passes, stream);
 }
 
 // ---- allocation-free decode ----------------------------------------------------
