@@ -36,42 +36,6 @@ constexpr int kWoRows = 64;     // output rows per workgroup
 constexpr int kWoThreads = 256;
 constexpr int kWoWaves = kWoThreads / kWave;
 
-// C consecutive weights of one row, as f32.
-template <int WT, int C>
-__device__ inline void load_weights(const uint8_t *src, float (&x)[C]) {
-    if constexpr (WT == SFA_KV_F16) {
-        if constexpr (C % 8 == 0) {
-#pragma unroll
-            for (int i = 0; i < C / 8; ++i) {
-                const half8 h = reinterpret_cast<const half8 *>(src)[i];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)h[j];
-            }
-        } else if constexpr (C % 2 == 0) {
-#pragma unroll
-            for (int i = 0; i < C / 2; ++i) {
-                const half2v h = reinterpret_cast<const half2v *>(src)[i];
-                x[2 * i] = (float)h[0];
-                x[2 * i + 1] = (float)h[1];
-            }
-        } else {
-            x[0] = (float)*reinterpret_cast<const _Float16 *>(src);
-        }
-    } else {
-        if constexpr (C % 4 == 0) {
-#pragma unroll
-            for (int i = 0; i < C / 4; ++i) {
-                const floatx4 v = reinterpret_cast<const floatx4 *>(src)[i];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) x[4 * i + j] = v[j];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < C; ++i) x[i] = reinterpret_cast<const float *>(src)[i];
-        }
-    }
-}
-
 __device__ inline void store_through(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
@@ -79,14 +43,49 @@ __device__ inline float load_through(const float *p) {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-template <int HD, int G, int WT>
-__global__ __launch_bounds__(kWoThreads) void merge_wo_kernel(DecodeParams p, WoParams w) {
+// Raw weights: C consecutive elements of one row as loaded (f16 stays packed
+// until used, which halves the registers holding the wave's rows).
+template <int WT, int C>
+struct WRow {
+    static constexpr int kWords = (C * (WT == SFA_KV_F16 ? 2 : 4) + 3) / 4;
+    uint32_t u[kWords];
+    __device__ inline void load(const uint8_t *src) {
+        if constexpr (kWords % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < kWords / 4; ++i) {
+                const intx4 v = reinterpret_cast<const intx4 *>(src)[i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) u[4 * i + j] = (uint32_t)v[j];
+            }
+        } else if constexpr (WT == SFA_KV_F16 && C == 1) {
+            u[0] = *reinterpret_cast<const uint16_t *>(src);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kWords; ++i) u[i] = reinterpret_cast<const uint32_t *>(src)[i];
+        }
+    }
+    __device__ inline float at(int i) const {
+        if constexpr (WT == SFA_KV_F16) {
+            const uint16_t h = (uint16_t)(u[i / 2] >> (16 * (i % 2)));
+            return (float)__builtin_bit_cast(_Float16, h);
+        } else {
+            return __builtin_bit_cast(float, u[i]);
+        }
+    }
+};
+
+// ONE: a single sequence (no loop over sequences: the loads of its records, its
+// plan and the rows of wo then sit in one straight line of code, and the waits
+// for each are exact).
+template <int HD, int G, int WT, bool ONE>
+__global__ __launch_bounds__(kWoThreads, G * HD <= 512 ? 2 : 1) void merge_wo_kernel(DecodeParams p, WoParams w) {
     constexpr int K = G * HD;          // inputs of one kv head's slice of wo
     constexpr int C = K / kWave;       // of them per lane
     constexpr int RW = kWoRows / kWoWaves;  // rows per wave
     constexpr int ES = WT == SFA_KV_F16 ? 2 : 4;
     constexpr int VPT = (K + kWoThreads - 1) / kWoThreads;  // merged values per thread
-    constexpr int SB = 32;             // split records loaded per batch
+    constexpr int SB = 16;             // split records loaded per batch
+    constexpr int MR = kMaxSplits / kWave;  // (m, l) registers per lane
     static_assert(C >= 1 && K % kWave == 0, "slice of at least one input per lane");
     __shared__ float lds_o[K];
     __shared__ float lds_wt[G][kMaxSplits];
@@ -105,68 +104,113 @@ __global__ __launch_bounds__(kWoThreads) void merge_wo_kernel(DecodeParams p, Wo
     const uint8_t *wcol = w.wo + (int64_t)kvh * K * ES + (int64_t)lane * C * ES;
     const int wrow0 = rb * kWoRows + wave * RW;  // this wave's first row
 
-    // the wave's rows of wo, this lane's C inputs of each: loaded once, before
-    // anything waits, and reused for every sequence (rows past n_embd read row 0)
-    float wv[RW][C];
+    // a sequence's split records: the (m, l) of every split of the wave's
+    // heads and the thread's values' first SB partial rows, all loaded before
+    // any of them is needed; indices clamp into the row, so every load is in
+    // bounds, and records past the sequence's splits get weight zero
+    float mv[(G + kWoWaves - 1) / kWoWaves][MR], lv[(G + kWoWaves - 1) / kWoWaves][MR];
+    float ob[VPT][SB];
+    auto load_records = [&](const float *pg, int n_rec) {
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const int row = wrow0 + r < w.n_embd ? wrow0 + r : 0;
-        load_weights<WT, C>(wcol + (int64_t)row * in_stride, wv[r]);
+        for (int gi = 0; gi * kWoWaves < G; ++gi) {
+            const int g = wave + gi * kWoWaves;
+            if (g < G) {
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    const int s = min(kWave * r + lane, n_rec - 1);
+                    mv[gi][r] = pg[(int64_t)s * sstride + g * (HD + 4) + HD];
+                    lv[gi][r] = pg[(int64_t)s * sstride + g * (HD + 4) + HD + 1];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int v = min(tid + kWoThreads * k, K - 1);
+            const float *col = pg + (v / HD) * (HD + 4) + v % HD;
+#pragma unroll
+            for (int u = 0; u < SB; ++u) ob[k][u] = col[(int64_t)min(u, n_rec - 1) * sstride];
+        }
+    };
+    // Issue order matters: loads complete in issue order, so the small loads
+    // the merge waits on (seq_len, and for one sequence its split records,
+    // which it owns from slot 0 of its kv head's row and can fetch before the
+    // plan is known) go out before the wave's rows of wo, which stream in
+    // from HBM while the merge runs.  The rows (this lane's C inputs of each;
+    // rows past n_embd read row 0) are reused for every sequence.
+    // one sequence: its plan from seq_len[0] / kv_lo[0] (scalar loads), as
+    // plan_lanes computes it for B = 1; a batch: the general plan
+    int one_n_kv = 0, one_lo = 0;
+    PlanRaw raw{0, 0};
+    if constexpr (ONE) {
+        one_n_kv = p.seq_len[0];
+        one_lo = p.kv_lo ? p.kv_lo[0] : 0;
+        load_records(row0, p.split_row);
+    } else {
+        raw = plan_load(p, lane);
     }
+    WRow<WT, C> wv[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) wv[r].load(wcol + (int64_t)(wrow0 + r < w.n_embd ? wrow0 + r : 0) * in_stride);
 
-    const PlanRaw raw = plan_load(p, lane);
-    for (int b = 0; b < p.n_seq; ++b) {
+    for (int b = 0; b < (ONE ? 1 : p.n_seq); ++b) {
         SlotPlan sp;
-        plan(p, raw, 0, b, lane, sp);
+        if constexpr (ONE) {
+            sp.g = seq_geom(one_n_kv, one_lo, p.max_pages * p.page_size);
+            sp.n_b = splits_of(sp.g.n_tiles, p.one_split ? 0 : p.split_row - 1, sp.g.n_tiles);
+            sp.rec0 = 0;
+        } else {
+            plan(p, raw, 0, b, lane, sp);
+        }
         const int n_b = sp.n_b;
         const float *pg = row0 + (int64_t)sp.rec0 * sstride;
         // ---- the attention output of this kv head's g heads -> lds_o
         if (n_b > 1) {
-            // split weights 2^(m_s - M) per head, in the merge pass's arithmetic
-            // (zero for s >= n_b)
-            for (int g = wave; g < G; g += kWoWaves) {
-                float mv[kMaxSplits / kWave], lv[kMaxSplits / kWave];
-                float mx = -INFINITY;
+            if constexpr (!ONE) load_records(pg, n_b);
+            // split weights 2^(m_s - M) per head, the merge pass's arithmetic
 #pragma unroll
-                for (int r = 0; r < kMaxSplits / kWave; ++r) {
-                    const int s = kWave * r + lane;
-                    const int sc = s < n_b ? s : n_b - 1;  // clamped: every load stays in the record row
-                    const float m0 = pg[(int64_t)sc * sstride + g * (HD + 4) + HD];
-                    mv[r] = s < n_b ? m0 : -INFINITY;
-                    lv[r] = pg[(int64_t)sc * sstride + g * (HD + 4) + HD + 1];
-                    mx = fmaxf(mx, mv[r]);
-                }
-                const float M = wave_max(mx);
-                float lsum = 0.0f;
+            for (int gi = 0; gi * kWoWaves < G; ++gi) {
+                const int g = wave + gi * kWoWaves;
+                if (g < G) {
+                    float mx = -INFINITY;
 #pragma unroll
-                for (int r = 0; r < kMaxSplits / kWave; ++r) {
-                    const float wt = mv[r] != -INFINITY ? __builtin_amdgcn_exp2f(mv[r] - M) : 0.0f;
-                    lsum += wt != 0.0f ? lv[r] * wt : 0.0f;
-                    lds_wt[g][kWave * r + lane] = wt;
+                    for (int r = 0; r < MR; ++r) {
+                        mv[gi][r] = kWave * r + lane < n_b ? mv[gi][r] : -INFINITY;
+                        mx = fmaxf(mx, mv[gi][r]);
+                    }
+                    const float M = wave_max(mx);
+                    float lsum = 0.0f;
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) {
+                        const float wt = mv[gi][r] != -INFINITY ? __builtin_amdgcn_exp2f(mv[gi][r] - M) : 0.0f;
+                        lsum += wt != 0.0f ? lv[gi][r] * wt : 0.0f;
+                        lds_wt[g][kWave * r + lane] = wt;
+                    }
+                    const float L = wave_sum(lsum);
+                    if (lane == 0) lds_l[g] = L;
                 }
-                const float L = wave_sum(lsum);
-                if (lane == 0) lds_l[g] = L;
             }
             __syncthreads();
-            // each thread's values: SB records' loads in flight at a time,
-            // accumulated in split order (clamped records past n_b weigh 0)
+            // accumulate in split order: the first SB records are in registers,
+            // later ones (long sequences) load batch by batch
 #pragma unroll
             for (int k = 0; k < VPT; ++k) {
                 const int v = tid + kWoThreads * k;
                 if (v < K) {
-                    const int g = v / HD, d = v % HD;
-                    const float *col = pg + g * (HD + 4) + d;
+                    const int g = v / HD;
+                    const float *col = pg + g * (HD + 4) + v % HD;
                     float O = 0.0f;
-                    for (int s0 = 0; s0 < n_b; s0 += SB) {
+#pragma unroll
+                    for (int u = 0; u < SB; ++u) {
+                        const float wt = lds_wt[g][u];
+                        O = wt != 0.0f ? fmaf(ob[k][u], wt, O) : O;
+                    }
+                    for (int s0 = SB; s0 < n_b; s0 += SB) {
                         float o[SB];
 #pragma unroll
-                        for (int u = 0; u < SB; ++u) {
-                            const int s = s0 + u < n_b ? s0 + u : n_b - 1;
-                            o[u] = col[(int64_t)s * sstride];
-                        }
+                        for (int u = 0; u < SB; ++u) o[u] = col[(int64_t)min(s0 + u, n_b - 1) * sstride];
 #pragma unroll
                         for (int u = 0; u < SB; ++u) {
-                            const float wt = s0 + u < kMaxSplits ? lds_wt[g][s0 + u] : 0.0f;
+                            const float wt = lds_wt[g][s0 + u];
                             O = wt != 0.0f ? fmaf(o[u], wt, O) : O;
                         }
                     }
@@ -178,12 +222,12 @@ __global__ __launch_bounds__(kWoThreads) void merge_wo_kernel(DecodeParams p, Wo
             }
         } else {
             // one split: the split pass wrote the output; none: zero
-            const float *ob = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
+            const float *obuf = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
 #pragma unroll
             for (int k = 0; k < VPT; ++k) {
                 const int v = tid + kWoThreads * k;
                 if (v < K) {
-                    float x = n_b == 1 ? ob[v] : 0.0f;
+                    float x = n_b == 1 ? obuf[v] : 0.0f;
                     if constexpr (WT == SFA_KV_F16) x = (float)(_Float16)x;
                     lds_o[v] = x;
                 }
@@ -191,7 +235,14 @@ __global__ __launch_bounds__(kWoThreads) void merge_wo_kernel(DecodeParams p, Wo
         }
         __syncthreads();
 
-        // ---- this kv head's partial sums of the wave's rows
+        // ---- this kv head's partial sums of the wave's rows.  The empty asm
+        // keeps the f16 -> f32 conversions of the rows here: hoisted out of
+        // the sequence loop they would wait for the rows before the merge.
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+#pragma unroll
+            for (int j = 0; j < WRow<WT, C>::kWords; ++j) asm volatile("" : "+v"(wv[r].u[j]));
+        }
         float ov[C];
 #pragma unroll
         for (int i = 0; i < C; ++i) ov[i] = lds_o[lane * C + i];
@@ -200,7 +251,7 @@ __global__ __launch_bounds__(kWoThreads) void merge_wo_kernel(DecodeParams p, Wo
         for (int r = 0; r < RW; ++r) {
             float a = 0.0f;
 #pragma unroll
-            for (int i = 0; i < C; ++i) a = fmaf(wv[r][i], ov[i], a);
+            for (int i = 0; i < C; ++i) a = fmaf(wv[r].at(i), ov[i], a);
             acc[r] = a;
         }
 #pragma unroll
@@ -263,10 +314,14 @@ static int launch_wo(const DecodeParams &p, const WoParams &w, int wo_type, hipS
         return SFA_ERR_UNSUPPORTED;
     } else {
         const dim3 grid(p.n_head_kv * w.n_rb), block(kWoThreads);
-        if (wo_type == SFA_KV_F16)
-            hipLaunchKernelGGL((merge_wo_kernel<HD, G, SFA_KV_F16>), grid, block, 0, s, p, w);
-        else
-            hipLaunchKernelGGL((merge_wo_kernel<HD, G, SFA_KV_F32>), grid, block, 0, s, p, w);
+        const bool one = p.n_seq == 1;
+        if (wo_type == SFA_KV_F16) {
+            if (one) hipLaunchKernelGGL((merge_wo_kernel<HD, G, SFA_KV_F16, true>), grid, block, 0, s, p, w);
+            else hipLaunchKernelGGL((merge_wo_kernel<HD, G, SFA_KV_F16, false>), grid, block, 0, s, p, w);
+        } else {
+            if (one) hipLaunchKernelGGL((merge_wo_kernel<HD, G, SFA_KV_F32, true>), grid, block, 0, s, p, w);
+            else hipLaunchKernelGGL((merge_wo_kernel<HD, G, SFA_KV_F32, false>), grid, block, 0, s, p, w);
+        }
         return SFA_OK;
     }
 }
