@@ -84,10 +84,13 @@ __device__ inline uint32_t load4_a4(const uint8_t *p) {
 struct PageWindow {
     int base;
     int32_t ids;
+    // The load is unconditional (a clamped index, then a select): a load in a
+    // branch makes the compiler's wait at the join count every later load too.
     __device__ inline void load(const int32_t *pt, int max_pages, int first, int lane) {
         base = first;
         const int lp = first + lane;
-        ids = lp < max_pages ? pt[lp] : -1;
+        const int32_t id = pt[lp < max_pages ? lp : max_pages - 1];
+        ids = lp < max_pages ? id : -1;
     }
     __device__ inline int32_t get(const int32_t *pt, int max_pages, int lp, int lane) {
         if (lp < base || lp >= base + kWave) load(pt, max_pages, lp, lane);

@@ -149,16 +149,19 @@ struct SlotPlan {
 struct PlanRaw {
     int n_kv, lo;
 };
+// Branch-free: every lane loads (clamped indices, then selects), so the
+// compiler can wait for exactly these loads and not for the ones issued after.
 __device__ inline PlanRaw plan_load(const DecodeParams &p, int lane) {
-    PlanRaw r{0, 0};
-    if (p.n_seq == 1) {
-        r.n_kv = p.seq_len[0];
-        r.lo = p.kv_lo ? p.kv_lo[0] : 0;
-    } else if (p.n_seq <= kWave && lane < p.n_seq) {
-        r.n_kv = p.seq_len[lane];
-        r.lo = p.kv_lo ? p.kv_lo[lane] : 0;
-    }
-    return r;
+    const int i = p.n_seq <= kWave ? (lane < p.n_seq ? lane : p.n_seq - 1) : 0;
+    // kv_lo or, when absent, a harmless re-read of seq_len; both are global
+    // memory (a generic-pointer load here would be a flat load, which the
+    // compiler's waits cannot count apart from the loads after it)
+    typedef const __attribute__((address_space(1))) int32_t *gptr;
+    const gptr lo_src = (gptr)(p.kv_lo ? p.kv_lo : p.seq_len);
+    const int32_t n = ((gptr)p.seq_len)[i];
+    const int32_t lo = lo_src[i];
+    const bool mine = p.n_seq == 1 || (p.n_seq <= kWave && lane < p.n_seq);
+    return PlanRaw{mine ? n : 0, (mine && p.kv_lo) ? lo : 0};
 }
 
 // Sequence b = -1 asks for the owner of row slot j (false: the slot is idle);

@@ -108,7 +108,12 @@ __device__ inline void split_merge(float (*lds_m)[G], float (*lds_l)[G], float (
     }
 }
 
-template <int HD, int G>
+// ONE: a single sequence.  Its plan then comes from seq_len[0] / kv_lo[0]
+// through scalar loads, and the prologue is straight-line code, so the one
+// wait before the first tile's K/V requests is for the page-id load alone
+// (the Q loads stay in flight): a load inside a branch would make the
+// compiler's wait at the join count every later load.
+template <int HD, int G, bool ONE>
 __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
     static_assert(G >= 1 && G <= 32 && (32 % G) == 0, "group size");
@@ -145,31 +150,42 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
     // Issues the K (A operand: row n, dims 16c + 8hh) and V (coalesced: row
-    // i*RPI + lane/CPR, chunk lane%CPR) loads of tile t.  The loads do not
-    // depend on seq_len: every row of a tile lies in one existing page, and
-    // rows outside [lo, n_kv) are masked after arrival (score -inf, V zeroed).
-    // Returns false (wave-uniform) when the tile's page id is invalid.
+    // i*RPI + lane/CPR, chunk lane%CPR) loads of tile t, whose page id is pid
+    // (wave-uniform).  The loads do not depend on seq_len: every row of a tile
+    // lies in one existing page, and rows outside [lo, n_kv) are masked after
+    // arrival (score -inf, V zeroed).  They are buffer loads over the tile's
+    // rows, issued unconditionally: an invalid page id gets a descriptor of
+    // zero bytes, whose loads return zeros and read nothing.  Returns false
+    // (wave-uniform) for an invalid page.
     half8 kf[KC];
     half8 vr[VIT];
     PageWindow pages;
-    auto issue = [&](int t) -> bool {
+    const int k_lane = n * (int)col_bytes + 16 * hh;
+    const int v_lane = (lane / CPR) * (int)col_bytes + 16 * (lane % CPR);
+    auto issue = [&](int t, int32_t pid) -> bool {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
-        if (lpage >= p.max_pages) return false;
-        const int32_t pid = pages.get(pt, p.max_pages, lpage, lane);
         const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
         const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
-        if (kb == nullptr || vb == nullptr) return false;
+        const bool ok = lpage < p.max_pages && kb != nullptr && vb != nullptr;
         const int64_t off0 = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
-        const uint8_t *kr = kb + off0 + (int64_t)n * col_bytes + 16 * hh;
+        const int n_rec = ok ? (kTile - 1) * (int)col_bytes + p.row_bytes : 0;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(ok ? kb + off0 : p.k_pages), 0, n_rec, kBufferRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(ok ? vb + off0 : p.v_pages), 0, n_rec, kBufferRsrcWord3);
 #pragma unroll
-        for (int c = 0; c < KC; ++c) kf[c] = *reinterpret_cast<const half8 *>(kr + 32 * c);
+        for (int c = 0; c < KC; ++c)
+            kf[c] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, k_lane + 32 * c, 0, 0));
 #pragma unroll
-        for (int i = 0; i < VIT; ++i) {
-            const int r = i * RPI + lane / CPR;
-            vr[i] = *reinterpret_cast<const half8 *>(vb + off0 + (int64_t)r * col_bytes + 16 * (lane % CPR));
-        }
-        return true;
+        for (int i = 0; i < VIT; ++i)
+            vr[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rv, v_lane + i * RPI * (int)col_bytes, 0, 0));
+        return ok;
+    };
+    auto page_of = [&](int t) -> int32_t {
+        const int lpage = t * kTile / p.page_size;
+        return lpage < p.max_pages ? pages.get(pt, p.max_pages, lpage, lane) : -1;
     };
 
     // Prologue order matters: loads complete in issue order (one vmcnt), so
@@ -182,7 +198,16 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
     t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave);
     pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
-    const PlanRaw raw = plan_load(p, lane);
+    // one sequence: seq_len / kv_lo through scalar loads (a counter of their
+    // own); a batch: per-lane loads
+    int one_n_kv = 0, one_lo = 0;
+    PlanRaw raw{0, 0};
+    if constexpr (ONE) {
+        one_n_kv = p.seq_len[0];
+        one_lo = p.kv_lo ? p.kv_lo[0] : 0;
+    } else {
+        raw = plan_load(p, lane);
+    }
     // Q of the g heads rounded to f16 (the F16 vec_dot_type conversion ggml
     // applies to src1), staged once per workgroup in LDS; the Q^T operand of
     // column n (head n % g, dims 16c + 8hh .. +8) is re-read per tile, which
@@ -190,19 +215,31 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     static_assert(G * HD / 8 <= 256, "one Q chunk per thread");
     const bool q_thread = threadIdx.x < G * HD / 8;
     floatx4 qx0 = floatx4{}, qx1 = floatx4{};
+    // every thread loads (the spare ones re-read chunk 0): no branch around it
     auto load_q = [&](int bq) {
-        if (q_thread) {
-            const floatx4 *qr = reinterpret_cast<const floatx4 *>(
-                p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
-            qx0 = qr[2 * threadIdx.x];
-            qx1 = qr[2 * threadIdx.x + 1];
-        }
+        const floatx4 *qr = reinterpret_cast<const floatx4 *>(
+            p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
+        const int c = q_thread ? (int)threadIdx.x : 0;
+        qx0 = qr[2 * c];
+        qx1 = qr[2 * c + 1];
     };
     load_q(b_g);
-    bool tile_ok = issue(t_guess);
+    // the window starts at the guessed tile's page: its id is lane 0's
+    bool tile_ok = issue(t_guess, __builtin_amdgcn_readlane(pages.ids, 0));
 
     SlotPlan sp;
-    if (!plan(p, raw, slot, -1, lane, sp)) {
+    bool active;
+    if constexpr (ONE) {
+        sp.g = seq_geom(one_n_kv, one_lo, p.max_pages * p.page_size);
+        sp.n_b = splits_of(sp.g.n_tiles, p.one_split ? 0 : p.split_row - 1, sp.g.n_tiles);
+        sp.b = 0;
+        sp.rec0 = 0;
+        sp.split = slot;
+        active = slot < sp.n_b;
+    } else {
+        active = plan(p, raw, slot, -1, lane, sp);
+    }
+    if (!active) {
         // an idle slot; the merge pass writes the output of a sequence
         // without tiles, or, for one sequence, the slot that would own it
         if (p.n_seq == 1 && slot == 0 && sp.n_b == 0) {
@@ -229,7 +266,7 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     const int lo = sp.g.lo, n_kv = sp.g.n_kv;
     float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
     int t = tile_lo + wave_u;
-    if (t != t_guess || b != b_g) tile_ok = t < tile_hi ? issue(t) : false;
+    if (t != t_guess || b != b_g) tile_ok = t < tile_hi ? issue(t, page_of(t)) : false;
     __syncthreads();
     const half8 *qrow = reinterpret_cast<const half8 *>(lds_q) + (n % G) * (HD / 8) + hh;
 
@@ -268,7 +305,7 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
             }
         }
         // registers are free: start the next tile's loads now
-        const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves) : false;
+        const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves, page_of(t + kDecodeWaves)) : false;
 
         // online softmax (log2 domain); row of register i is tile position
         // 8(i/4) + 4hh + i%4.  Interior tiles need no mask.  The reference
@@ -641,7 +678,10 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
 // drift apart, so a barrier every other loop trip (four tiles) keeps them in
 // step (B = 8 over 8k..32k: 452 -> 392 MiB read per layer; a barrier every
 // trip reads 377 MiB but waits longer than it saves).
-template <int HD, int G, bool COLS>
+// ONE (per-kv-head layout only): a single sequence, planned from seq_len[0] /
+// kv_lo[0] through scalar loads, with a straight-line prologue (see the f16
+// kernel).
+template <int HD, int G, bool COLS, bool ONE>
 __global__ __launch_bounds__(COLS ? 64 * kColsWaves : 256, (COLS || G <= 4) ? 2 : 1)
 void decode_q8_kernel(DecodeParams p) {
     static_assert(HD == 64 || HD == 128, "head_dim");
@@ -696,44 +736,90 @@ void decode_q8_kernel(DecodeParams p) {
         uint32_t vw[VBL][9];         // the 36 bytes around each V block
     };
     PageWindow pages;
-    auto issue = [&](int t, Raw &r) -> bool {
+    // Tile t's loads (page id pid, wave-uniform) are buffer loads over the
+    // kv head's rows of the tile, issued unconditionally: an invalid page gets
+    // a zero-byte descriptor (loads return zeros, nothing is read) and false.
+    // Every offset is 4-byte aligned (rows are 136 or 68 bytes, columns a
+    // multiple of 4, blocks at 34c or 34c + 2 as below).
+    const int row_lane = n * (int)col_bytes;
+    auto issue = [&](int t, Raw &r, int32_t pid) -> bool {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
-        if (lpage >= p.max_pages) return false;
-        const int32_t pid = pages.get(pt, p.max_pages, lpage, lane);
         const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
         const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
-        if (kb == nullptr || vb == nullptr) return false;
-        const int64_t off = (int64_t)(pos0 - lpage * p.page_size + n) * col_bytes + (int64_t)kvh * p.row_bytes;
-        const uint8_t *kr = kb + off;
-        const uint8_t *vr = vb + off;
+        const bool ok = lpage < p.max_pages && kb != nullptr && vb != nullptr;
+        const int64_t off = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
+        if constexpr (COLS) {
+            // the column layout keeps plain global loads after one page check
+            // (with the buffer loads below, or a check per load, the compiler's
+            // waits drain the other register set: 104 -> 130 us per B = 8 step)
+            if (!ok) return false;
+            const uint8_t *kr = kb + off + row_lane;
+            const uint8_t *vr = vb + off + row_lane;
+#pragma unroll
+            for (int c = 0; c < NB; ++c) {
+                if ((c & 1) == 0) {
+                    const uint8_t *w = kr + 34 * c + 16 * hh;
+                    r.kw[c] = load16_a4(w);
+                    r.kx[c / 2] = load4_a4(w + 16);
+                    r.kd[c] = load4_a4(kr + 34 * c);
+                } else {
+                    r.kw[c] = load16_a4(kr + 34 * c + 2 + 16 * hh);
+                    r.kd[c] = load4_a4(kr + 34 * c - 2);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < VBL; ++u) {
+                const int c = VBL * hh + u;
+                const uint8_t *w = vr + 34 * c - (c & 1) * 2;
+                const intx4 a0 = load16_a4(w), a1 = load16_a4(w + 16);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { r.vw[u][j] = (uint32_t)a0[j]; r.vw[u][4 + j] = (uint32_t)a1[j]; }
+                r.vw[u][8] = load4_a4(w + 32);
+            }
+            return true;
+        }
+        const int n_rec = ok ? (kTile - 1) * (int)col_bytes + p.row_bytes : 0;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(ok ? kb + off : p.k_pages), 0, n_rec, kBufferRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(ok ? vb + off : p.v_pages), 0, n_rec, kBufferRsrcWord3);
+        auto ld16 = [&](__amdgpu_buffer_rsrc_t rs, int o) {
+            return __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rs, row_lane + o, 0, 0));
+        };
+        auto ld4 = [&](__amdgpu_buffer_rsrc_t rs, int o) {
+            return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, row_lane + o, 0, 0);
+        };
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
             if ((c & 1) == 0) {
                 // block at 34c (4-aligned): quants of half hh start 2 bytes
                 // into the dword at 34c + 16hh; d is the low half at 34c
-                const uint8_t *w = kr + 34 * c + 16 * hh;
-                r.kw[c] = load16_a4(w);
-                r.kx[c / 2] = load4_a4(w + 16);
-                r.kd[c] = load4_a4(kr + 34 * c);
+                r.kw[c] = ld16(rk, 34 * c + 16 * hh);
+                r.kx[c / 2] = ld4(rk, 34 * c + 16 * hh + 16);
+                r.kd[c] = ld4(rk, 34 * c);
             } else {
                 // block at 34c (2 mod 4): quants 4-aligned; d is the high half
                 // of the dword at 34c - 2
-                r.kw[c] = load16_a4(kr + 34 * c + 2 + 16 * hh);
-                r.kd[c] = load4_a4(kr + 34 * c - 2);
+                r.kw[c] = ld16(rk, 34 * c + 2 + 16 * hh);
+                r.kd[c] = ld4(rk, 34 * c - 2);
             }
         }
 #pragma unroll
         for (int u = 0; u < VBL; ++u) {
             const int c = VBL * hh + u;
-            // 9 dwords from the 4-aligned address at or 2 bytes below the block
-            const uint8_t *w = vr + 34 * c - (c & 1) * 2;
-            const intx4 a0 = load16_a4(w), a1 = load16_a4(w + 16);
+            // 9 dwords from the 4-aligned offset at or 2 bytes below the block
+            const int w = 34 * c - (c & 1) * 2;
+            const intx4 a0 = ld16(rv, w), a1 = ld16(rv, w + 16);
 #pragma unroll
             for (int j = 0; j < 4; ++j) { r.vw[u][j] = (uint32_t)a0[j]; r.vw[u][4 + j] = (uint32_t)a1[j]; }
-            r.vw[u][8] = load4_a4(w + 32);
+            r.vw[u][8] = ld4(rv, w + 32);
         }
-        return true;
+        return ok;
+    };
+    auto page_of = [&](int t) -> int32_t {
+        const int lpage = t * kTile / p.page_size;
+        return lpage < p.max_pages ? pages.get(pt, p.max_pages, lpage, lane) : -1;
     };
 
     // Prologue order as in the f16 kernel: page-id window, seq_len / kv_lo
@@ -742,10 +828,18 @@ void decode_q8_kernel(DecodeParams p) {
     split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
     t_guess = __builtin_amdgcn_readfirstlane(t_guess + wave_u);
     pages.load(pt, p.max_pages, t_guess * kTile / p.page_size, lane);
-    const PlanRaw raw = plan_load(p, lane);
+    int one_n_kv = 0, one_lo = 0;
+    PlanRaw raw{0, 0};
+    if constexpr (ONE) {
+        one_n_kv = p.seq_len[0];
+        one_lo = p.kv_lo ? p.kv_lo[0] : 0;
+    } else {
+        raw = plan_load(p, lane);
+    }
     // Q of the g heads of a kv head, one 8-element chunk per thread (one load
     // of each Q value per workgroup: per-lane copies would queue ahead of the
-    // first tile's K/V requests); COLS: each wave its own kv head's chunks
+    // first tile's K/V requests); COLS: each wave its own kv head's chunks.
+    // Spare threads re-read the last chunk (no branch around the loads).
     static_assert(G * HD / 8 <= 256, "one Q chunk per thread");
     constexpr int QCH = COLS ? (G * HD / 8 + 63) / 64 : 1;  // chunks per thread
     const int q_idx0 = COLS ? lane : (int)threadIdx.x;
@@ -755,17 +849,29 @@ void decode_q8_kernel(DecodeParams p) {
             p.q + ((int64_t)bq * p.n_head + (int64_t)kvh * G) * HD);
 #pragma unroll
         for (int k = 0; k < QCH; ++k) {
-            const int idx = q_idx0 + 64 * k;
-            qx0[k] = idx < G * HD / 8 ? qr[2 * idx] : floatx4{};
-            qx1[k] = idx < G * HD / 8 ? qr[2 * idx + 1] : floatx4{};
+            const int idx = min(q_idx0 + 64 * k, G * HD / 8 - 1);
+            qx0[k] = qr[2 * idx];
+            qx1[k] = qr[2 * idx + 1];
         }
     };
     load_q(b_g);
     Raw ra, rb;
-    bool ok_a = issue(t_guess, ra);
+    // the window starts at the guessed tile's page: its id is lane 0's
+    bool ok_a = issue(t_guess, ra, __builtin_amdgcn_readlane(pages.ids, 0));
 
     SlotPlan sp;
-    if (!plan(p, raw, slot, -1, lane, sp)) {
+    bool active;
+    if constexpr (ONE) {
+        sp.g = seq_geom(one_n_kv, one_lo, p.max_pages * p.page_size);
+        sp.n_b = splits_of(sp.g.n_tiles, p.one_split ? 0 : p.split_row - 1, sp.g.n_tiles);
+        sp.b = 0;
+        sp.rec0 = 0;
+        sp.split = slot;
+        active = slot < sp.n_b;
+    } else {
+        active = plan(p, raw, slot, -1, lane, sp);
+    }
+    if (!active) {
         // an idle slot; the merge pass writes the output of a sequence
         // without tiles, or, for one sequence, the slot that would own it
         if (p.n_seq == 1 && slot == 0 && sp.n_b == 0) {
@@ -822,7 +928,7 @@ void decode_q8_kernel(DecodeParams p) {
                       // i.e. rows 4hh + i, head (4hh + i) % G, read per tile)
 
     int t = tile_lo + wave_u;
-    if (t != t_guess || b != b_g) ok_a = t < tile_hi ? issue(t, ra) : false;
+    if (t != t_guess || b != b_g) ok_a = t < tile_hi ? issue(t, ra, page_of(t)) : false;
 
     floatx16 o[DB];
 #pragma unroll
@@ -1008,11 +1114,11 @@ void decode_q8_kernel(DecodeParams p) {
     for (; t < tile_hi; t += 2 * TS) {
         const int t1 = t + TS;
         if (ok_a) consume1(t, ra, sv);
-        const bool ok_b = t1 < tile_hi ? issue(t1, rb) : false;
+        const bool ok_b = t1 < tile_hi ? issue(t1, rb, page_of(t1)) : false;
         if (ok_a) consume2(t, sv);
         if (t1 >= tile_hi) break;
         if (ok_b) consume1(t1, rb, sv);
-        ok_a = t1 + TS < tile_hi ? issue(t1 + TS, ra) : false;
+        ok_a = t1 + TS < tile_hi ? issue(t1 + TS, ra, page_of(t1 + TS)) : false;
         if (ok_b) consume2(t1, sv);
         // column layout: every wave has the same tiles; keep them in step so
         // the cache lines that neighbouring kv heads share are fetched once
@@ -1070,7 +1176,7 @@ void decode_q8_kernel(DecodeParams p) {
 // A batch sequence without tiles gets a zero output here.  The code is
 // branch-free straight-line work: the pass is latency-bound and each taken
 // branch or instruction-cache miss adds to it.
-template <int HD, int G>
+template <int HD, int G, bool ONE>
 __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeParams p) {
     constexpr int CH = kWave;                       // splits per round
     constexpr int RMAX = (kMaxSplits + CH - 1) / CH;  // (m, l) registers per lane
@@ -1082,40 +1188,50 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     const int d = tid < HD ? tid : HD - 1;  // threads past HD (HD < 64) only load (m, l)
     const int sstride = G * (HD + 4);
     const float *row0 = p.part + (int64_t)kvh * p.split_row * sstride + g * (HD + 4);
-    // one sequence owns the row from slot 0, so its records are fetched
-    // before seq_len is read; in a batch the plan places them first
-    const PlanRaw raw = plan_load(p, lane);
-    SlotPlan sp;
-    int rec0 = 0, S = p.split_row;
-    if (p.n_seq > 1) {
+
+    float o[CH];
+    float mv[RMAX], lv[RMAX];
+    // the rows of splits s0 .. s0 + CH - 1 of the sequence's records at pg,
+    // indices clamped to the S records (wave-uniform, always in bounds)
+    auto load_round = [&](const float *pg, int s0, int S) {
+#pragma unroll
+        for (int u = 0; u < CH; ++u) o[u] = pg[(int64_t)min(s0 + u, S - 1) * sstride + d];
+    };
+    auto load_ml = [&](const float *pg, int S) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            const int s = min(CH * r + lane, S - 1);
+            mv[r] = pg[(int64_t)s * sstride + HD];
+            lv[r] = pg[(int64_t)s * sstride + HD + 1];
+        }
+    };
+    int n_active, rec0 = 0, S;
+    if constexpr (ONE) {
+        // one sequence owns the row from slot 0: every load of the first CH
+        // splits and the (m, l) of all goes out before seq_len (scalar loads,
+        // their own counter) is known
+        S = p.split_row;
+        load_round(row0, 0, S);
+        load_ml(row0, S);
+        const SeqGeom sg = seq_geom(p.seq_len[0], p.kv_lo ? p.kv_lo[0] : 0, p.max_pages * p.page_size);
+        n_active = splits_of(sg.n_tiles, p.one_split ? 0 : p.split_row - 1, sg.n_tiles);
+    } else {
+        // in a batch the plan (from every seq_len) places the sequence's
+        // records in the row first
+        const PlanRaw raw = plan_load(p, lane);
+        SlotPlan sp;
         plan_lanes(p, raw, 0, b, lane, sp);  // per-lane selects below; no scalar copy needed
         rec0 = sp.rec0;
         S = sp.n_b > 0 ? sp.n_b : 1;
+        n_active = sp.n_b;
+        load_round(row0 + (int64_t)rec0 * sstride, 0, S);
+        load_ml(row0 + (int64_t)rec0 * sstride, S);
     }
     const float *pg = row0 + (int64_t)rec0 * sstride;
-
-    float o[CH];
-    auto load_round = [&](int s0) {
-#pragma unroll
-        for (int u = 0; u < CH; ++u) {
-            const float *row = pg + (int64_t)min(s0 + u, S - 1) * sstride;  // wave-uniform
-            o[u] = row[d];
-        }
-    };
-    load_round(0);
-    float mv[RMAX], lv[RMAX];
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-        const int s = min(CH * r + lane, S - 1);
-        mv[r] = pg[s * sstride + HD];
-        lv[r] = pg[s * sstride + HD + 1];
-    }
-    if (p.n_seq == 1) plan_lanes(p, raw, 0, 0, lane, sp);
-    const int n_active = sp.n_b;
     if (n_active <= 1) {
         // one split: written by the split pass; none (a batch sequence with
         // no tiles): the output is zero
-        if (n_active == 0 && p.n_seq > 1 && tid < HD)
+        if (!ONE && n_active == 0 && tid < HD)
             p.out[((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD + tid] = 0.0f;
         return;
     }
@@ -1141,7 +1257,7 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
         if (CH * r >= n_active) break;
-        if (r > 0) load_round(CH * r);
+        if (r > 0) load_round(pg, CH * r, S);
 #pragma unroll
         for (int u = 0; u < CH; ++u) {
             const float wt = lane_val(w[r], u);
@@ -1215,9 +1331,14 @@ size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
 
 template <int HD, int G>
 static void launch_merge(const DecodeParams &p, int B, int Hkv, int passes, hipStream_t s) {
-    if ((passes & 2) && !p.one_split)
-        hipLaunchKernelGGL((decode_merge_kernel<HD, G>), dim3(B * Hkv * G), dim3(kMergeThreads<HD>), 0,
-                           s, p);
+    if ((passes & 2) && !p.one_split) {
+        if (B == 1)
+            hipLaunchKernelGGL((decode_merge_kernel<HD, G, true>), dim3(Hkv * G), dim3(kMergeThreads<HD>), 0,
+                               s, p);
+        else
+            hipLaunchKernelGGL((decode_merge_kernel<HD, G, false>), dim3(B * Hkv * G),
+                               dim3(kMergeThreads<HD>), 0, s, p);
+    }
 }
 
 // pass bit 1: split-K pass, bit 2: merge pass
@@ -1228,17 +1349,25 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
         if (p.kv_type == SFA_KV_Q8_0) {
             if constexpr (HD >= 64 && G <= 4) {
                 if (p.cols_waves > 0) {
-                    hipLaunchKernelGGL((decode_q8_kernel<HD, G, true>), dim3(p.split_row * (Hkv / p.cols_waves)),
+                    hipLaunchKernelGGL((decode_q8_kernel<HD, G, true, false>), dim3(p.split_row * (Hkv / p.cols_waves)),
                                        dim3(64 * p.cols_waves), 0, s, p);
                     return launch_merge<HD, G>(p, B, Hkv, passes, s);
                 }
             }
             if constexpr (HD >= 64 && G <= 8)
-                hipLaunchKernelGGL((decode_q8_kernel<HD, G, false>), grid, dim3(256), 0, s, p);
+            {
+                if (B == 1)
+                    hipLaunchKernelGGL((decode_q8_kernel<HD, G, false, true>), grid, dim3(256), 0, s, p);
+                else
+                    hipLaunchKernelGGL((decode_q8_kernel<HD, G, false, false>), grid, dim3(256), 0, s, p);
+            }
         } else if (p.kv_type == SFA_KV_F32) {
             hipLaunchKernelGGL((decode_f32_kernel<HD, G>), grid, dim3(256), 0, s, p);
         } else {
-            hipLaunchKernelGGL((decode_f16_kernel<HD, G>), grid, dim3(256), 0, s, p);
+            if (B == 1)
+                hipLaunchKernelGGL((decode_f16_kernel<HD, G, true>), grid, dim3(256), 0, s, p);
+            else
+                hipLaunchKernelGGL((decode_f16_kernel<HD, G, false>), grid, dim3(256), 0, s, p);
         }
     }
     launch_merge<HD, G>(p, B, Hkv, passes, s);
