@@ -197,10 +197,20 @@ def load_traffic() -> dict:
 
 
 def with_traffic(roofline: dict, key: str) -> dict:
+    """Adds the profiled HBM bytes per launch and the rocprofv3 mean duration
+    of the same kernel on the same workload, with the achieved rate and frac
+    computed from that mean (beside the live figures, which use HIP events
+    around back-to-back launches)."""
     t = load_traffic().get(key)
     if t:
         roofline["traffic"] = t["bytes_per_launch"]
         roofline["traffic_source"] = f"profiles/traffic.json[{key}] (rocprofv3 FETCH_SIZE+WRITE_SIZE)"
+        work = roofline.get("bytes_per_launch") or roofline.get("flop_per_launch")
+        if work and t.get("kernel_us_mean"):
+            ach = work / (t["kernel_us_mean"] * 1e-6) / (1e9 if roofline["unit"] == "GB/s" else 1e12)
+            roofline["rocprof"] = {"kernel_us_mean": t["kernel_us_mean"], "achieved": round(ach, 1),
+                                   "frac": round(ach / roofline["peak"], 4),
+                                   "source": t.get("profile") or "profiles/"}
     return roofline
 
 
@@ -231,8 +241,9 @@ def decode_leg(torch, key, lens, kv_type, steps, warmup, seed, cpu_budget_s: flo
     us_layer = ms * 1e3 / N_LAYER
     # Q8_0 batches of two or more with >= 1024 tiles in all run the column layout
     cols = kv_type == 8 and len(lens) >= 2 and len(lens) * ((mx + 31) // 32) >= 1024
-    kname = {0: "decode_f32_kernel<128,4>", 1: "decode_f16_kernel<128,4>",
-             8: f"decode_q8_kernel<128,4,{'true' if cols else 'false'}>"}[kv_type]
+    one = "true" if len(lens) == 1 else "false"
+    kname = {0: "decode_f32_kernel<128,4>", 1: f"decode_f16_kernel<128,4,{one}>",
+             8: "decode_q8_kernel<128,4,true,false>" if cols else f"decode_q8_kernel<128,4,false,{one}>"}[kv_type]
     res = {
         "workload": f"decode-attn {KV_NAMES[kv_type]} KV, Mixtral GQA 32q/8kv hd128, "
                     f"B={len(lens)}, context {lens if len(lens) > 1 else lens[0]}, 256-token pages "
@@ -365,7 +376,8 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1, c
                                   "peak": peak, "unit": "TFLOP/s",
                                   "frac": round(tflops / peak, 4), "traffic": None,
                                   "kernel": {0: "prefill_f32_kernel<128,4>", 1: "prefill_f16_kernel<128,4>",
-                                             8: "prefill_q8_kernel<128,4>"}[kv_type]},
+                                             8: "prefill_q8_kernel<128,4>"}[kv_type],
+                                  "flop_per_launch": flops},
                                  {1: "prefill_2048_on_2048", 0: "prefill_f32_2048_on_2048",
                                   8: "prefill_q8_0_2048_on_2048"}[kv_type]),
         "flop_per_layer_chunk": flops,
@@ -435,6 +447,12 @@ def decode_wo_bench(torch, steps: int, warmup: int, seed: int):
                      "kernel": "split-K pass + merge_wo_kernel<128,4,f16> (the node, graph-replayed)",
                      "bytes_per_launch": alg,
                      "what": "K + V + Q + wo + residual + y once, over the node's time"},
+        # the fused second pass alone: wo once, the split records once, residual in, y out
+        "merge_wo_kernel": with_traffic({"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                         "frac": None, "traffic": None,
+                                         "kernel": "merge_wo_kernel<128,4,f16,true>",
+                                         "bytes_per_launch": n_embd * HQ * HD * 2 + HKV * 32 * 4 * (HD + 4) * 4
+                                         + 2 * n_embd * 4}, "decode_wo_f16"),
     }
     del kv, q, wo
     torch.cuda.empty_cache()
@@ -596,7 +614,7 @@ def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 8, cp
             "hbm_bytes_per_layer_step": hbm + qo,
             "host_link_bytes_per_layer_step": link,
         }
-        kname = "decode_f16_kernel<128,4> (split-K pass)"
+        kname = "decode_f16_kernel<128,4,false> (split-K pass)"
         if attend == SFA_ATTEND_WINDOW:
             entry["roofline"] = hbm_roofline(hbm + qo, k_mean, us, kname, "window_sliding")
         else:
@@ -821,6 +839,8 @@ def main():
                     help="seconds of timed CPU work per thread count and CPU leg")
     ap.add_argument("--window-lossless-steps", type=int, default=8, metavar="N",
                     help="decode steps of the lossless window leg (N-1 timed)")
+    ap.add_argument("--window-steps", type=int, default=128, metavar="N",
+                    help="decode steps of the sliding-window leg (N-1 timed)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0 decode legs")
     ap.add_argument("--no-window", action="store_true", help="skip the KV-window paging legs")
@@ -873,7 +893,8 @@ def main():
         elif args.only == "wo":
             r = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
         else:
-            r = window_bench(torch, args.seed + 3, lossless_steps=args.window_lossless_steps)
+            r = window_bench(torch, args.seed + 3, steps=args.window_steps,
+                             lossless_steps=args.window_lossless_steps)
         print(json.dumps({args.only: r}))
         return
 
@@ -885,7 +906,7 @@ def main():
     us_layer = ms_step * 1e3 / N_LAYER
     kv_bytes = 2 * ctx * HKV * HD * 2
     alg_bytes = kv_bytes + HQ * HD * 4 * 2  # K + V + Q + O, each once
-    roof = hbm_roofline(alg_bytes, k_mean, us_layer, "decode_f16_kernel<128,4> (split-K pass)",
+    roof = hbm_roofline(alg_bytes, k_mean, us_layer, "decode_f16_kernel<128,4,true> (split-K pass)",
                         "decode_f16_ctx4096")
     roof["kernel_us_median"] = round(k_med, 3)
 
@@ -929,7 +950,8 @@ def main():
     if not args.no_q8:
         result["q8_0"] = q8_bench(torch, max(args.steps // 4, 5), 3, args.seed + 2, cpu_budget_s=cpu_s)
     if not args.no_window:
-        result["window"] = window_bench(torch, args.seed + 3, lossless_steps=args.window_lossless_steps,
+        result["window"] = window_bench(torch, args.seed + 3, steps=args.window_steps,
+                                        lossless_steps=args.window_lossless_steps,
                                         cpu_budget_s=cpu_s)
     if not args.no_rope:
         result["rope_append"] = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
