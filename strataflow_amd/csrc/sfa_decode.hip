@@ -153,35 +153,31 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     // i*RPI + lane/CPR, chunk lane%CPR) loads of tile t, whose page id is pid
     // (wave-uniform).  The loads do not depend on seq_len: every row of a tile
     // lies in one existing page, and rows outside [lo, n_kv) are masked after
-    // arrival (score -inf, V zeroed).  They are buffer loads over the tile's
-    // rows, issued unconditionally: an invalid page id gets a descriptor of
-    // zero bytes, whose loads return zeros and read nothing.  Returns false
-    // (wave-uniform) for an invalid page.
+    // arrival (score -inf, V zeroed).  Returns false (wave-uniform), loading
+    // nothing, for an invalid page.  Plain global loads: buffer loads over the
+    // tile's rows (a zero-byte descriptor for an invalid page, no branch) made
+    // the prologue no faster and the loop slower (B = 1, context 32768: split
+    // pass 28.9 -> 30.0 us).
     half8 kf[KC];
     half8 vr[VIT];
     PageWindow pages;
-    const int k_lane = n * (int)col_bytes + 16 * hh;
-    const int v_lane = (lane / CPR) * (int)col_bytes + 16 * (lane % CPR);
     auto issue = [&](int t, int32_t pid) -> bool {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
+        if (lpage >= p.max_pages) return false;
         const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
         const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
-        const bool ok = lpage < p.max_pages && kb != nullptr && vb != nullptr;
+        if (kb == nullptr || vb == nullptr) return false;
         const int64_t off0 = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh * p.row_bytes;
-        const int n_rec = ok ? (kTile - 1) * (int)col_bytes + p.row_bytes : 0;
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(ok ? kb + off0 : p.k_pages), 0, n_rec, kBufferRsrcWord3);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(ok ? vb + off0 : p.v_pages), 0, n_rec, kBufferRsrcWord3);
+        const uint8_t *kr = kb + off0 + (int64_t)n * col_bytes + 16 * hh;
 #pragma unroll
-        for (int c = 0; c < KC; ++c)
-            kf[c] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, k_lane + 32 * c, 0, 0));
+        for (int c = 0; c < KC; ++c) kf[c] = *reinterpret_cast<const half8 *>(kr + 32 * c);
 #pragma unroll
-        for (int i = 0; i < VIT; ++i)
-            vr[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rv, v_lane + i * RPI * (int)col_bytes, 0, 0));
-        return ok;
+        for (int i = 0; i < VIT; ++i) {
+            const int r = i * RPI + lane / CPR;
+            vr[i] = *reinterpret_cast<const half8 *>(vb + off0 + (int64_t)r * col_bytes + 16 * (lane % CPR));
+        }
+        return true;
     };
     auto page_of = [&](int t) -> int32_t {
         const int lpage = t * kTile / p.page_size;
