@@ -45,6 +45,15 @@ EXPORTS = (
     "sfa_page_table_check",
 )
 
+# include/sfa_layer.h (the rest of the decode layer; also in libsfa.so)
+LAYER_EXPORTS = (
+    "sfa_rms_norm",
+    "sfa_mul_mat_vec",
+    "sfa_moe_route",
+    "sfa_moe_workspace_bytes",
+    "sfa_moe_ffn",
+)
+
 
 class SfaKvDesc(ctypes.Structure):
     _fields_ = [
@@ -123,6 +132,17 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_attn_prefill.restype = ctypes.c_int
     lib.sfa_page_table_check.argtypes = [D, P, i32, P, P, i32]
     lib.sfa_page_table_check.restype = ctypes.c_int
+    # the rest of the decode layer (include/sfa_layer.h)
+    lib.sfa_rms_norm.argtypes = [P, P, P, i32, i32, ctypes.c_float, P]
+    lib.sfa_rms_norm.restype = ctypes.c_int
+    lib.sfa_mul_mat_vec.argtypes = [P, i32, P, P, P, i32, i32, i32, P]
+    lib.sfa_mul_mat_vec.restype = ctypes.c_int
+    lib.sfa_moe_route.argtypes = [P, i32, i32, i32, P, P, P]
+    lib.sfa_moe_route.restype = ctypes.c_int
+    lib.sfa_moe_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.sfa_moe_workspace_bytes.restype = ctypes.c_size_t
+    lib.sfa_moe_ffn.argtypes = [P, P, P, P, P, P, P, i32, i32, i32, i32, i32, i32, P, ctypes.c_size_t, P, P]
+    lib.sfa_moe_ffn.restype = ctypes.c_int
     _lib = lib
     return lib
 

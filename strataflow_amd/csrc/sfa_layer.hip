@@ -1,0 +1,456 @@
+// sfa_layer.hip - the rest of the decode layer around the attention node, for
+// gfx950: build_router_segment and build_expert_segment of the reference
+// (src/model/engine/engine.cpp:1877-1925, 1945-1986) as four kernels.
+//
+//   attn_norm / ffn_norm   rms_norm(x, eps) * weight             engine.cpp:1879-1880, 1908-1909
+//   Q/K/V, wo, router      mul_mat(W, x) (+ residual)            engine.cpp:1883-1885, 1905-1906, 1912
+//   routing                soft_max, argsort_top_k, get_rows,
+//                          sum_rows, clamp, div                  engine.cpp:1913-1925
+//   experts                mul_mat_id(up/gate), swiglu_split,
+//                          mul_mat_id(down), * weights, sum,
+//                          + residual                            engine.cpp:1964-1984
+//
+// Arithmetic follows ggml's CPU backend, the reference's oracle: rms_norm sums
+// the f32 squares in double and scales by 1/sqrtf(mean + eps); mul_mat with F16
+// weights first rounds the activation row to f16 (the vec_dot_type of F16) and
+// sums f16 x f16 products in f32; soft_max sums exp(x - max) in double and
+// scales by (float)(1/sum); sum_rows sums in double; the expert outputs are
+// multiplied by their weights, added in slot order, then the residual is added.
+//
+// Every kernel is HBM-bound at decode (one or a few tokens per weight read):
+// a wave owns four output rows and its lanes stream each row in 16-byte
+// chunks, so one wave keeps 4 rows x 4 chunks x 1 KB in flight; activations
+// (a few KB) come from L2.  Weights are row-major [n_out][n_in] (ggml ne =
+// [n_in, n_out]); expert stacks are [n_expert][n_out][n_in].
+#include <exception>
+
+#include "sfa_common.h"
+#include "sfa_layer.h"
+
+namespace sfa {
+
+constexpr int kRowsPerWave = 4;
+constexpr int kLayerWaves = 4;
+constexpr int kRowsPerBlock = kRowsPerWave * kLayerWaves;
+
+// 8 consecutive activations as the f16 operand of F16 weights (RNE, the
+// FP32 -> FP16 conversion ggml applies to src1)
+__device__ inline half8 to_half8(const floatx4 a, const floatx4 b) {
+    half8 h;
+    h[0] = (_Float16)a[0]; h[1] = (_Float16)a[1]; h[2] = (_Float16)a[2]; h[3] = (_Float16)a[3];
+    h[4] = (_Float16)b[0]; h[5] = (_Float16)b[1]; h[6] = (_Float16)b[2]; h[7] = (_Float16)b[3];
+    return h;
+}
+
+struct Half2x4 {
+    half2v v[4];  // the four dwords of a half8
+};
+
+// sum of 8 products: f16 x f16 through v_dot2_f32_f16 (exact products, f32
+// accumulation), f32 x f32 by fma
+__device__ inline float dot8(const half8 w, const half8 x, float acc) {
+    const Half2x4 a = __builtin_bit_cast(Half2x4, w), b = __builtin_bit_cast(Half2x4, x);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2(a.v[j], b.v[j], acc, false);
+    return acc;
+}
+__device__ inline float dot8(const floatx4 w0, const floatx4 w1, const floatx4 x0, const floatx4 x1, float acc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(w0[j], x0[j], acc);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(w1[j], x1[j], acc);
+    return acc;
+}
+
+// ---- rms_norm * weight --------------------------------------------------------
+
+// One workgroup per row: y = (x * (1/sqrtf(mean(x^2) + eps))) * w, the two
+// products rounded separately (ggml_rms_norm, then ggml_mul).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const float *w, float *y, int n,
+                                                       float eps) {
+    __shared__ double part[kLayerWaves];
+    const float *xr = x + (int64_t)blockIdx.x * n;
+    float *yr = y + (int64_t)blockIdx.x * n;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = xr[i];
+        s += (double)(v * v);
+    }
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    double t = 0.0;
+    for (int k = 0; k < (int)(blockDim.x >> 6); ++k) t += part[k];
+    const float mean = (float)(t / n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+}
+
+// ---- mul_mat_vec ---------------------------------------------------------------
+
+struct GemvParams {
+    const void *w;         // [n_out][n_in], f32 or f16
+    const float *x;        // [n_rows][n_in]
+    const float *residual; // [n_rows][n_out] or null
+    float *y;              // [n_rows][n_out]
+    int n_rows, n_in, n_out;
+};
+
+// Wave w of block b owns rows 16b + 4w .. +3 (clamped to n_out - 1 for the
+// loads, not stored) for NT tokens starting at token blockIdx.y * NT.
+template <bool F16, int NT>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (int)blockIdx.x * kRowsPerBlock + wave * kRowsPerWave;
+    const int tok0 = (int)blockIdx.y * NT;
+    const int nc = p.n_in / 8;  // 8-element chunks per row
+    float acc[kRowsPerWave][NT];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[r][t] = 0.0f;
+    int rows[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) rows[r] = min(row0 + r, p.n_out - 1);
+    int toks[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) toks[t] = min(tok0 + t, p.n_rows - 1);
+
+#pragma unroll 4
+    for (int c = lane; c < nc; c += 64) {
+        if constexpr (F16) {
+            const half8 *W = static_cast<const half8 *>(p.w);
+            half8 wv[kRowsPerWave];
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) wv[r] = W[(int64_t)rows[r] * nc + c];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)toks[t] * p.n_in) + 2 * c;
+                const half8 xh = to_half8(xr[0], xr[1]);
+#pragma unroll
+                for (int r = 0; r < kRowsPerWave; ++r) acc[r][t] = dot8(wv[r], xh, acc[r][t]);
+            }
+        } else {
+            const floatx4 *W = static_cast<const floatx4 *>(p.w);
+            floatx4 w0[kRowsPerWave], w1[kRowsPerWave];
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) {
+                w0[r] = W[((int64_t)rows[r] * nc + c) * 2];
+                w1[r] = W[((int64_t)rows[r] * nc + c) * 2 + 1];
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)toks[t] * p.n_in) + 2 * c;
+                const floatx4 x0 = xr[0], x1 = xr[1];
+#pragma unroll
+                for (int r = 0; r < kRowsPerWave; ++r) acc[r][t] = dot8(w0[r], w1[r], x0, x1, acc[r][t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float v = wave_sum(acc[r][t]);
+            if (lane == r * NT + t && row0 + r < p.n_out && tok0 + t < p.n_rows) {
+                const int64_t o = (int64_t)(tok0 + t) * p.n_out + row0 + r;
+                p.y[o] = p.residual ? __fadd_rn(v, p.residual[o]) : v;
+            }
+        }
+    }
+}
+
+// ---- routing --------------------------------------------------------------------
+
+// One wave per token, lane e holding expert e (n_expert <= 64): probabilities,
+// the n_used largest in descending order (ties: the lower expert first, a
+// stable descending argsort), their weights divided by their sum clamped at
+// 2^-14.
+__global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int n_expert, int n_used,
+                                                       int32_t *ids, float *weights) {
+    const int lane = threadIdx.x;
+    const float *lr = logits + (int64_t)blockIdx.x * n_expert;
+    const bool live = lane < n_expert;
+    const float x = live ? lr[lane] : -INFINITY;
+    const float mx = wave_max(x);
+    const float e = live ? expf(x - mx) : 0.0f;
+    double s = (double)e;
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    const float inv = (float)(1.0 / s);
+    const float pr = __fmul_rn(e, inv);
+    bool taken = !live;
+    float wsel = 0.0f;  // lane j < n_used: the j-th selected probability
+    int esel = 0;
+    for (int j = 0; j < n_used; ++j) {
+        const float cand = taken ? -INFINITY : pr;
+        const float best = wave_max(cand);
+        const uint64_t hit = __ballot(!taken && cand == best);
+        const int pick = hit ? __builtin_ctzll(hit) : 0;
+        const float pv = __shfl(pr, pick, 64);
+        if (lane == j) { wsel = pv; esel = pick; }
+        taken = taken || lane == pick;
+    }
+    double ws = lane < n_used ? (double)wsel : 0.0;
+    for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off, 64);
+    float sum = (float)ws;
+    sum = sum < 6.103515625e-5f ? 6.103515625e-5f : sum;
+    if (lane < n_used) {
+        ids[(int64_t)blockIdx.x * n_used + lane] = esel;
+        weights[(int64_t)blockIdx.x * n_used + lane] = __fdiv_rn(wsel, sum);
+    }
+}
+
+// ---- experts --------------------------------------------------------------------
+
+struct MoeParams {
+    const float *x;          // [n_rows][n_embd] (ffn_norm output)
+    const float *residual;   // [n_rows][n_embd] (ffn_inp)
+    const int32_t *ids;      // [n_rows][n_used]
+    const float *weights;    // [n_rows][n_used]
+    const void *gate, *up;   // [n_expert][n_ff][n_embd]
+    const void *down;        // [n_expert][n_embd][n_ff]
+    float *act;              // [n_rows][n_used][n_ff]
+    float *y;                // [n_rows][n_embd]
+    int n_rows, n_embd, n_ff, n_expert, n_used;
+};
+
+// act[t][j][f] = silu(gate[e][f] . x[t]) * (up[e][f] . x[t]), e = ids[t][j];
+// an id outside [0, n_expert) gives zeros.  Grid (row blocks of n_ff, n_used,
+// n_rows).
+template <bool F16>
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int f0 = (int)blockIdx.x * kRowsPerBlock + wave * kRowsPerWave;
+    const int j = blockIdx.y, t = blockIdx.z;
+    const int e_raw = p.ids[(int64_t)t * p.n_used + j];
+    const bool valid = e_raw >= 0 && e_raw < p.n_expert;
+    const int e = valid ? e_raw : 0;
+    const int nc = p.n_embd / 8;
+    float g[kRowsPerWave], u[kRowsPerWave];
+    int rows[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        g[r] = u[r] = 0.0f;
+        rows[r] = min(f0 + r, p.n_ff - 1);
+    }
+    const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)t * p.n_embd);
+    const int64_t mat = (int64_t)e * p.n_ff;
+#pragma unroll 4
+    for (int c = lane; c < nc; c += 64) {
+        if constexpr (F16) {
+            const half8 *G = static_cast<const half8 *>(p.gate), *U = static_cast<const half8 *>(p.up);
+            half8 gv[kRowsPerWave], uv[kRowsPerWave];
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) {
+                gv[r] = G[(mat + rows[r]) * nc + c];
+                uv[r] = U[(mat + rows[r]) * nc + c];
+            }
+            const half8 xh = to_half8(xr[2 * c], xr[2 * c + 1]);
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) {
+                g[r] = dot8(gv[r], xh, g[r]);
+                u[r] = dot8(uv[r], xh, u[r]);
+            }
+        } else {
+            const floatx4 *G = static_cast<const floatx4 *>(p.gate), *U = static_cast<const floatx4 *>(p.up);
+            floatx4 g0[kRowsPerWave], g1[kRowsPerWave], u0[kRowsPerWave], u1[kRowsPerWave];
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) {
+                const int64_t o = ((mat + rows[r]) * nc + c) * 2;
+                g0[r] = G[o]; g1[r] = G[o + 1];
+                u0[r] = U[o]; u1[r] = U[o + 1];
+            }
+            const floatx4 x0 = xr[2 * c], x1 = xr[2 * c + 1];
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) {
+                g[r] = dot8(g0[r], g1[r], x0, x1, g[r]);
+                u[r] = dot8(u0[r], u1[r], x0, x1, u[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        const float gs = wave_sum(g[r]), us = wave_sum(u[r]);
+        if (lane == r && f0 + r < p.n_ff) {
+            // ggml_silu_f32(x) = x / (1 + expf(-x)), times up (swiglu_split)
+            const float a = __fmul_rn(__fdiv_rn(gs, __fadd_rn(1.0f, expf(-gs))), us);
+            p.act[((int64_t)t * p.n_used + j) * p.n_ff + f0 + r] = valid ? a : 0.0f;
+        }
+    }
+}
+
+// y[t][o] = (sum over slots j in order of (down[e_j][o] . act[t][j]) * w[t][j])
+// + residual[t][o]; a slot with an id outside [0, n_expert) adds nothing.
+// Grid (row blocks of n_embd, n_rows).
+template <bool F16>
+__global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int o0 = (int)blockIdx.x * kRowsPerBlock + wave * kRowsPerWave;
+    const int t = blockIdx.y;
+    const int nc = p.n_ff / 8;
+    int rows[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) rows[r] = min(o0 + r, p.n_embd - 1);
+    float out[kRowsPerWave];
+    for (int j = 0; j < p.n_used; ++j) {
+        const int e_raw = p.ids[(int64_t)t * p.n_used + j];
+        const bool valid = e_raw >= 0 && e_raw < p.n_expert;
+        const int e = valid ? e_raw : 0;
+        const float wj = p.weights[(int64_t)t * p.n_used + j];
+        const floatx4 *ar = reinterpret_cast<const floatx4 *>(p.act + ((int64_t)t * p.n_used + j) * p.n_ff);
+        const int64_t mat = (int64_t)e * p.n_embd;
+        float d[kRowsPerWave];
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) d[r] = 0.0f;
+#pragma unroll 4
+        for (int c = lane; c < nc; c += 64) {
+            if constexpr (F16) {
+                const half8 *D = static_cast<const half8 *>(p.down);
+                half8 dv[kRowsPerWave];
+#pragma unroll
+                for (int r = 0; r < kRowsPerWave; ++r) dv[r] = D[(mat + rows[r]) * nc + c];
+                const half8 ah = to_half8(ar[2 * c], ar[2 * c + 1]);
+#pragma unroll
+                for (int r = 0; r < kRowsPerWave; ++r) d[r] = dot8(dv[r], ah, d[r]);
+            } else {
+                const floatx4 *D = static_cast<const floatx4 *>(p.down);
+                floatx4 d0[kRowsPerWave], d1[kRowsPerWave];
+#pragma unroll
+                for (int r = 0; r < kRowsPerWave; ++r) {
+                    d0[r] = D[((mat + rows[r]) * nc + c) * 2];
+                    d1[r] = D[((mat + rows[r]) * nc + c) * 2 + 1];
+                }
+                const floatx4 a0 = ar[2 * c], a1 = ar[2 * c + 1];
+#pragma unroll
+                for (int r = 0; r < kRowsPerWave; ++r) d[r] = dot8(d0[r], d1[r], a0, a1, d[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+            const float v = valid ? __fmul_rn(wave_sum(d[r]), wj) : 0.0f;
+            out[r] = j == 0 ? v : __fadd_rn(out[r], v);
+        }
+    }
+    if (lane < kRowsPerWave && o0 + lane < p.n_embd) {
+        float v = out[0];
+#pragma unroll
+        for (int r = 1; r < kRowsPerWave; ++r) v = lane == r ? out[r] : v;
+        const int64_t o = (int64_t)t * p.n_embd + o0 + lane;
+        p.y[o] = __fadd_rn(v, p.residual[o]);
+    }
+}
+
+// ---- host side -------------------------------------------------------------------
+
+static int grid_x(int n) { return (n + kRowsPerBlock - 1) / kRowsPerBlock; }
+
+static int gemv_launch(const GemvParams &p, bool f16, hipStream_t s) {
+    const int nt = p.n_rows >= 8 ? 8 : p.n_rows >= 4 ? 4 : p.n_rows >= 2 ? 2 : 1;
+    const dim3 grid(grid_x(p.n_out), (p.n_rows + nt - 1) / nt);
+#define SFA_GEMV(NT)                                                                        \
+    case NT:                                                                                \
+        if (f16) hipLaunchKernelGGL((gemv_kernel<true, NT>), grid, dim3(256), 0, s, p);    \
+        else hipLaunchKernelGGL((gemv_kernel<false, NT>), grid, dim3(256), 0, s, p);       \
+        break;
+    switch (nt) {
+        SFA_GEMV(1)
+        SFA_GEMV(2)
+        SFA_GEMV(4)
+        SFA_GEMV(8)
+    }
+#undef SFA_GEMV
+    return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+}
+
+static bool weight_type_ok(int t) { return t == SFA_KV_F32 || t == SFA_KV_F16; }
+
+}  // namespace sfa
+
+extern "C" {
+
+SFA_API int sfa_rms_norm(const float *x, const float *weight, float *y, int32_t n_rows, int32_t n_embd,
+                         float eps, void *stream) {
+    try {
+        if (x == nullptr || weight == nullptr || y == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows < 0 || n_embd <= 0 || !(eps >= 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows == 0) return SFA_OK;
+        hipLaunchKernelGGL(sfa::rms_norm_kernel, dim3(n_rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           x, weight, y, n_embd, eps);
+        return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
+SFA_API int sfa_mul_mat_vec(const void *w, int32_t w_type, const float *x, const float *residual, float *y,
+                            int32_t n_rows, int32_t n_in, int32_t n_out, void *stream) {
+    try {
+        if (w == nullptr || x == nullptr || y == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows < 0 || n_in <= 0 || n_out <= 0) return SFA_ERR_INVALID_ARGUMENT;
+        if (!sfa::weight_type_ok(w_type) || n_in % 8 != 0) return SFA_ERR_UNSUPPORTED;
+        if ((n_rows + 7) / 8 > 65535) return SFA_ERR_UNSUPPORTED;  // token blocks on grid y
+        if (n_rows == 0) return SFA_OK;
+        const sfa::GemvParams p{w, x, residual, y, n_rows, n_in, n_out};
+        return sfa::gemv_launch(p, w_type == SFA_KV_F16, static_cast<hipStream_t>(stream));
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
+SFA_API int sfa_moe_route(const float *logits, int32_t n_rows, int32_t n_expert, int32_t n_used,
+                          int32_t *ids, float *weights, void *stream) {
+    try {
+        if (logits == nullptr || ids == nullptr || weights == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows < 0 || n_expert <= 0 || n_used <= 0 || n_used > n_expert) return SFA_ERR_INVALID_ARGUMENT;
+        if (n_expert > 64) return SFA_ERR_UNSUPPORTED;
+        if (n_rows == 0) return SFA_OK;
+        hipLaunchKernelGGL(sfa::moe_route_kernel, dim3(n_rows), dim3(64), 0, static_cast<hipStream_t>(stream),
+                           logits, n_expert, n_used, ids, weights);
+        return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
+SFA_API size_t sfa_moe_workspace_bytes(int32_t n_rows, int32_t n_used, int32_t n_ff) {
+    if (n_rows <= 0 || n_used <= 0 || n_ff <= 0) return 0;
+    return (size_t)n_rows * n_used * n_ff * sizeof(float);
+}
+
+SFA_API int sfa_moe_ffn(const float *x, const float *residual, const int32_t *ids, const float *weights,
+                        const void *gate_exps, const void *up_exps, const void *down_exps, int32_t w_type,
+                        int32_t n_rows, int32_t n_embd, int32_t n_ff, int32_t n_expert, int32_t n_used,
+                        void *workspace, size_t ws_bytes, float *y, void *stream) {
+    try {
+        if (x == nullptr || residual == nullptr || ids == nullptr || weights == nullptr || y == nullptr)
+            return SFA_ERR_INVALID_ARGUMENT;
+        if (gate_exps == nullptr || up_exps == nullptr || down_exps == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows < 0 || n_embd <= 0 || n_ff <= 0 || n_expert <= 0 || n_used <= 0 || n_used > n_expert)
+            return SFA_ERR_INVALID_ARGUMENT;
+        if (!sfa::weight_type_ok(w_type) || n_embd % 8 != 0 || n_ff % 8 != 0) return SFA_ERR_UNSUPPORTED;
+        if (n_rows == 0) return SFA_OK;
+        if (workspace == nullptr || ws_bytes < sfa_moe_workspace_bytes(n_rows, n_used, n_ff))
+            return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows > 65535 || n_used > 65535) return SFA_ERR_UNSUPPORTED;
+        sfa::MoeParams p{x, residual, ids, weights, gate_exps, up_exps, down_exps, static_cast<float *>(workspace),
+                         y, n_rows, n_embd, n_ff, n_expert, n_used};
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        const bool f16 = w_type == SFA_KV_F16;
+        const dim3 g1(sfa::grid_x(n_ff), n_used, n_rows), g2(sfa::grid_x(n_embd), n_rows);
+        if (f16) {
+            hipLaunchKernelGGL(sfa::moe_gate_up_kernel<true>, g1, dim3(256), 0, s, p);
+            hipLaunchKernelGGL(sfa::moe_down_kernel<true>, g2, dim3(256), 0, s, p);
+        } else {
+            hipLaunchKernelGGL(sfa::moe_gate_up_kernel<false>, g1, dim3(256), 0, s, p);
+            hipLaunchKernelGGL(sfa::moe_down_kernel<false>, g2, dim3(256), 0, s, p);
+        }
+        return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
+}  // extern "C"

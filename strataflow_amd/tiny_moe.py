@@ -196,3 +196,80 @@ class HipAttention:
         else:
             out = self.kv.prefill(layer, tq, self.pt[0], pos0)
         return out.cpu().numpy()
+
+
+class TinyMoeGpu(TinyMoe):
+    """The whole forward on the GPU through libsfa.so, the decode layer of
+    build_router_segment + build_expert_segment (engine.cpp:1877-1986) op by
+    op: rms_norm * attn_norm; one product for Q, K and V (the three weights
+    stacked row-wise: the same dot products, one launch); RoPE of Q and K fused
+    with the KV append; attention with the wo projection and the residual fused
+    in for one token (sfa_attn_decode_wo), or the causal prefill then the wo
+    product for a chunk; rms_norm * ffn_norm; the router product; softmax top-k
+    routing; the SwiGLU experts with their weighted sum and the residual; the
+    output head.  Token ids go in and the last row's logits come out; nothing
+    else crosses the host link.  ``weight_dtype`` float16 rounds the weights
+    (a different model, for timing); float32 is the reference's."""
+
+    def __init__(self, cfg: TinyMoeConfig, weights: TinyMoeWeights, n_ctx: int, device: str = "cuda",
+                 seed: int = 0, kv_type: int | None = None, weight_dtype=None):
+        import torch
+
+        from .paged_kv import SFA_KV_F16, PagedKV
+        super().__init__(cfg, weights, attention=None)
+        self.torch, self.n_ctx, self.device = torch, n_ctx, device
+        wd = torch.float32 if weight_dtype is None else weight_dtype
+
+        def dev(a, dtype=torch.float32):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)
+
+        self.embd = dev(weights.token_embd)
+        self.output_norm = dev(weights.output_norm)
+        self.output = dev(weights.output, wd)
+        self.layers = []
+        for L in weights.layers:
+            self.layers.append(dict(
+                attn_norm=dev(L["attn_norm"]), ffn_norm=dev(L["ffn_norm"]),
+                wqkv=dev(np.concatenate([L["wq"], L["wk"], L["wv"]], axis=0), wd), wo=dev(L["wo"], wd),
+                gate_inp=dev(L["gate_inp"], wd), gate_exps=dev(L["gate_exps"], wd),
+                up_exps=dev(L["up_exps"], wd), down_exps=dev(L["down_exps"], wd)))
+        max_pages = (n_ctx + cfg.page_size - 1) // cfg.page_size
+        n_pages = max_pages + 3
+        self.kv = PagedKV(cfg.n_layer, cfg.n_head, cfg.n_head_kv, cfg.head_dim,
+                          SFA_KV_F16 if kv_type is None else kv_type, cfg.page_size, n_pages, device=device)
+        rng = np.random.default_rng(seed)
+        self.pt = torch.from_numpy(synth.page_tables(rng, [n_ctx], cfg.page_size, n_pages, max_pages)).to(device)
+        self._moe_ws = None
+
+    def forward(self, tokens, pos0: int) -> np.ndarray:
+        from . import layer as ops
+        torch, cfg = self.torch, self.cfg
+        dev = self.device
+        tok = torch.as_tensor(np.asarray(tokens, np.int64), device=dev)
+        T = int(tok.numel())
+        Hq, Hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+        pos = torch.arange(pos0, pos0 + T, dtype=torch.int32, device=dev)
+        seq = torch.zeros(T, dtype=torch.int32, device=dev)
+        sl = torch.tensor([pos0 + T], dtype=torch.int32, device=dev)
+        x = self.embd.index_select(0, tok)                                  # get_rows (engine.cpp:2712)
+        for il, L in enumerate(self.layers):
+            cur = ops.rms_norm(x, L["attn_norm"], cfg.rms_eps)
+            qkv = ops.mul_mat_vec(L["wqkv"], cur)
+            q = qkv[:, :Hq * hd].contiguous().view(T, Hq, hd)
+            k = qkv[:, Hq * hd:(Hq + Hkv) * hd].contiguous().view(T, Hkv, hd)
+            v = qkv[:, (Hq + Hkv) * hd:].contiguous().view(T, Hkv, hd)
+            self.kv.rope_append(il, q, k, v, seq, pos, self.pt, cfg.freq_base)
+            if T == 1:
+                ffn_inp = self.kv.decode_wo(il, q, self.pt, sl, self.n_ctx, L["wo"], x)
+            else:
+                attn = self.kv.prefill(il, q, self.pt[0], pos0)
+                ffn_inp = ops.mul_mat_vec(L["wo"], attn, residual=x)
+            cur = ops.rms_norm(ffn_inp, L["ffn_norm"], cfg.rms_eps)
+            ids, wts = ops.moe_route(ops.mul_mat_vec(L["gate_inp"], cur), cfg.n_expert_used)
+            need = T * cfg.n_expert_used * cfg.n_ff * 4
+            if self._moe_ws is None or self._moe_ws.numel() < need:
+                self._moe_ws = torch.empty(need, dtype=torch.uint8, device=dev)
+            x = ops.moe_ffn(cur, ffn_inp, ids, wts, L["gate_exps"], L["up_exps"], L["down_exps"],
+                            workspace=self._moe_ws)
+        h = ops.rms_norm(x[-1:].contiguous(), self.output_norm, cfg.rms_eps)
+        return ops.mul_mat_vec(self.output, h)[0].cpu().numpy()

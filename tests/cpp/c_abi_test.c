@@ -1,10 +1,11 @@
-/* The C ABI from plain C99: both headers compile as C, and the host-only entry
+/* The C ABI from plain C99: the headers compile as C, and the host-only entry
  * points (no GPU touched) behave as documented.  Built and run by
  * tests/test_c_abi.py; exit status 0 = pass. */
 #include <stdio.h>
 #include <string.h>
 
 #include "sfa.h"
+#include "sfa_layer.h"
 #include "sfa_pager.h"
 
 #define CHECK(cond)                                                   \
@@ -55,6 +56,15 @@ int main(void) {
         c.n_layer = 0;
         CHECK(sfa_pager_create(&c, &p) == SFA_ERR_INVALID_ARGUMENT && p == NULL);
         CHECK(sfa_pager_begin(NULL, NULL, NULL) == SFA_ERR_INVALID_ARGUMENT);
+    }
+    /* the layer entry points validate before any device work */
+    {
+        void *p = (void *)0x1000;
+        CHECK(sfa_moe_workspace_bytes(3, 2, 512) == (size_t)3 * 2 * 512 * 4);
+        CHECK(sfa_mul_mat_vec(p, SFA_KV_F16, (const float *)p, NULL, (float *)p, 1, 100, 64, NULL) ==
+              SFA_ERR_UNSUPPORTED);
+        CHECK(sfa_rms_norm(NULL, (const float *)p, (float *)p, 1, 256, 1e-5f, NULL) == SFA_ERR_INVALID_ARGUMENT);
+        CHECK(sfa_moe_route((const float *)p, 1, 8, 9, (int32_t *)p, (float *)p, NULL) == SFA_ERR_INVALID_ARGUMENT);
     }
     printf("c abi ok\n");
     return 0;

@@ -11,22 +11,45 @@ import pytest
 from strataflow_amd import _lib
 from strataflow_amd._lib import SfaKvDesc
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "sfa.h"
+INCLUDE = Path(__file__).resolve().parent.parent / "include"
+HEADER = INCLUDE / "sfa.h"
 
 
-def declared_symbols() -> set[str]:
-    text = HEADER.read_text()
+def declared_symbols(header: Path = HEADER) -> set[str]:
+    text = header.read_text()
     return set(re.findall(r"SFA_API\s+[\w\s\*]+?\b(sfa_\w+)\s*\(", text))
 
 
 def test_header_matches_binding_list():
     assert declared_symbols() == set(_lib.EXPORTS)
+    assert declared_symbols(INCLUDE / "sfa_layer.h") == set(_lib.LAYER_EXPORTS)
 
 
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
-    for name in declared_symbols():
+    for name in declared_symbols() | declared_symbols(INCLUDE / "sfa_layer.h"):
         assert hasattr(lib, name), name
+
+
+def test_layer_entry_points_validate_on_the_host():
+    """Argument checks return before any device work (no GPU needed)."""
+    lib = _lib.load()
+    F16, F32 = _lib.SFA_KV_F16, _lib.SFA_KV_F32
+    bad, uns = _lib.SFA_ERR_INVALID_ARGUMENT, _lib.SFA_ERR_UNSUPPORTED
+    p = 0x1000  # never dereferenced
+    assert lib.sfa_rms_norm(None, p, p, 1, 256, 1e-5, None) == bad
+    assert lib.sfa_rms_norm(p, p, p, 1, 0, 1e-5, None) == bad
+    assert lib.sfa_rms_norm(p, p, p, 0, 256, 1e-5, None) == _lib.SFA_OK  # nothing to do
+    assert lib.sfa_mul_mat_vec(p, F16, p, None, p, 1, 100, 64, None) == uns      # n_in % 8
+    assert lib.sfa_mul_mat_vec(p, 8, p, None, p, 1, 128, 64, None) == uns        # Q8_0 weights
+    assert lib.sfa_mul_mat_vec(p, F32, None, None, p, 1, 128, 64, None) == bad
+    assert lib.sfa_moe_route(p, 1, 65, 2, p, p, None) == uns                     # > 64 experts
+    assert lib.sfa_moe_route(p, 1, 8, 9, p, p, None) == bad                      # n_used > n_expert
+    assert lib.sfa_moe_workspace_bytes(2, 2, 512) == 2 * 2 * 512 * 4
+    assert lib.sfa_moe_workspace_bytes(0, 2, 512) == 0
+    ws = lib.sfa_moe_workspace_bytes(1, 2, 512)
+    assert lib.sfa_moe_ffn(p, p, p, p, p, p, p, F32, 1, 256, 512, 8, 2, p, ws - 4, p, None) == bad
+    assert lib.sfa_moe_ffn(p, p, p, p, p, p, p, F32, 1, 256, 500, 8, 2, p, ws, p, None) == uns
 
 
 def desc(**kw) -> SfaKvDesc:

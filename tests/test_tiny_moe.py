@@ -57,3 +57,24 @@ def test_tiny_moe_greedy_identical(gpu, oracle_mod, chunked, fused_rope, kv_type
           f"max per-step |dlogit|={dl:.3e} min top-2 margin={margin:.3e} tokens={got[0]}")
     assert same, (ref[0], got[0])
     assert dl < 1e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("chunked", [False, True], ids=["per_token_prompt", "chunked_prompt"])
+def test_tiny_moe_whole_layer_on_gpu(gpu, oracle_mod, chunked):
+    """Every op of the layer on the GPU (TinyMoeGpu: rms_norm, the Q/K/V product,
+    fused RoPE + append, attention with wo + residual fused, routing, SwiGLU
+    experts, the output head) against the host graph with the oracle's
+    attention: the same greedy sequence and the same per-step logit bar."""
+    from strataflow_amd.tiny_moe import TinyMoeGpu
+    cfg = TinyMoeConfig()
+    w = TinyMoeWeights(cfg, seed=0)
+    n_ctx = N_PROMPT + N_GEN
+    ref = TinyMoe(cfg, w, OracleAttention(oracle_mod, cfg, n_ctx, oracle_mod.GGML)).generate(
+        _prompt(cfg), N_GEN, chunked_prompt=chunked)
+    got = TinyMoeGpu(cfg, w, n_ctx, device=gpu).generate(_prompt(cfg), N_GEN, chunked_prompt=chunked)
+    same, dl, margin = _compare(ref, got)
+    print(f"\n[tiny-moe whole layer on GPU chunked={chunked}] seq match={same} "
+          f"max per-step |dlogit|={dl:.3e} min top-2 margin={margin:.3e}")
+    assert same, (ref[0], got[0])
+    assert dl < 1e-3
