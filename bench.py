@@ -393,8 +393,9 @@ def decode_wo_bench(torch, steps: int, warmup: int, seed: int):
     """The decode node with its consumer fused in (sfa_attn_decode_wo):
     y = wo @ attn + residual, wo f16 [4096, 4096] per layer (the Mixtral
     attn_output.weight shape), B=1, context 4096, 32 layers with distinct caches
-    and weights, graph-replayed.  Beside it the unfused chain: the decode node,
-    then the projection and the residual add as torch ops (f16 GEMV, casts, add)."""
+    and weights, graph-replayed.  Beside it two unfused chains: the decode node,
+    then the projection and the residual add as torch ops (f16 GEMV, casts,
+    add), or as one sfa_mul_mat_vec pass."""
     n_embd = HQ * HD
     kv, pt, t_pt, q, seq_len = build_decode_workload(torch, 4096, seed)
     dev = q.device
@@ -415,8 +416,15 @@ def decode_wo_bench(torch, steps: int, warmup: int, seed: int):
             kv.decode(layer, q[layer], t_pt, seq_len, 4096, out=attn[layer])
             y[layer] = torch.nn.functional.linear(attn[layer].half(), wo[layer]).float() + x[layer]
 
+    from strataflow_amd import layer as ops
+
+    def unfused_sfa():
+        for layer in range(N_LAYER):
+            kv.decode(layer, q[layer], t_pt, seq_len, 4096, out=attn[layer])
+            ops.mul_mat_vec(wo[layer], attn[layer], residual=x[layer], out=y[layer])
+
     res = {}
-    for name, fn in (("fused", fused), ("unfused", unfused)):
+    for name, fn in (("fused", fused), ("unfused", unfused), ("unfused_sfa", unfused_sfa)):
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -442,6 +450,8 @@ def decode_wo_bench(torch, steps: int, warmup: int, seed: int):
         "us_per_layer_token": round(res["fused"], 3),
         "us_per_layer_token_unfused": round(res["unfused"], 3),
         "unfused": "sfa_attn_decode, then torch f16 linear + cast + residual add",
+        "us_per_layer_token_unfused_sfa": round(res["unfused_sfa"], 3),
+        "unfused_sfa": "sfa_attn_decode, then sfa_mul_mat_vec (f16 wo, residual added in the same pass)",
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "split-K pass + merge_wo_kernel<128,4,f16> (the node, graph-replayed)",
@@ -457,6 +467,124 @@ def decode_wo_bench(torch, steps: int, warmup: int, seed: int):
     del kv, q, wo
     torch.cuda.empty_cache()
     return out
+
+
+def layer_bench(torch, steps: int, warmup: int, seed: int, n_layer: int = 8) -> dict:
+    """The whole decode layer on the GPU: n_layer Mixtral-shaped layers (n_embd
+    4096, 32 q / 8 kv heads of 128, 8 experts top-2, n_ff 14336; f16 weights
+    N(0,1)*0.02, distinct per layer) over distinct f16 caches at context 4096,
+    B = 1, one token per step through every layer, the step captured as one HIP
+    graph: rms_norm, the Q/K/V product (the three weights stacked), fused RoPE
+    + KV append, attention with wo + residual fused, rms_norm, the router
+    product, routing, the two routed experts' SwiGLU FFN and the residual.
+    The roofline counts the bytes a layer-token reads once: the Q/K/V, wo and
+    router weights, the two routed experts' gate, up and down rows, the KV
+    history (activations are a few KB)."""
+    from strataflow_amd import layer as ops
+    from strataflow_amd import synth
+    from strataflow_amd.paged_kv import SFA_KV_F16, PagedKV
+    dev = torch.device("cuda:0")
+    D, F, E, K, ctx = 4096, 14336, 8, 2, 4096
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+
+    def w(*shape):
+        return (torch.randn(shape, device=dev, generator=gen, dtype=torch.float16) * 0.02).contiguous()
+
+    layers = [dict(attn_norm=torch.ones(D, device=dev), ffn_norm=torch.ones(D, device=dev),
+                   wqkv=w((HQ + 2 * HKV) * HD, D), wo=w(D, HQ * HD), gate_inp=w(E, D),
+                   gate=w(E, F, D), up=w(E, F, D), down=w(E, D, F)) for _ in range(n_layer)]
+    pages = ctx // PAGE + 2
+    kv = PagedKV(n_layer, HQ, HKV, HD, SFA_KV_F16, PAGE, pages, device=dev)
+    rng = np.random.default_rng(seed)
+    pt = torch.from_numpy(synth.page_tables(rng, [ctx], PAGE, pages)).to(dev)
+    hist = ctx - 1
+    for il in range(n_layer):
+        pos = torch.arange(hist, device=dev, dtype=torch.int32)
+        kk = synth.rope_normal_torch(torch.randn((hist, HKV, HD), device=dev, generator=gen), pos, 1e6)
+        kv.append(il, kk.contiguous(), torch.randn((hist, HKV, HD), device=dev, generator=gen),
+                  torch.zeros(hist, device=dev, dtype=torch.int32), pos, pt)
+    x0 = torch.randn((1, D), device=dev, generator=gen)
+    x = torch.empty_like(x0)
+    cur, ffn_inp, qkv = torch.empty_like(x0), torch.empty_like(x0), torch.empty((1, (HQ + 2 * HKV) * HD), device=dev)
+    ids, wts = torch.empty((1, K), dtype=torch.int32, device=dev), torch.empty((1, K), device=dev)
+    moe_ws = torch.empty(K * F * 4, dtype=torch.uint8, device=dev)
+    pos1 = torch.tensor([hist], dtype=torch.int32, device=dev)
+    seq1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    sl = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    q = qkv[:, :HQ * HD].view(1, HQ, HD)
+    k = qkv[:, HQ * HD:(HQ + HKV) * HD].view(1, HKV, HD)
+    v = qkv[:, (HQ + HKV) * HD:].view(1, HKV, HD)
+
+    attn = torch.empty((1, HQ * HD), device=dev)
+
+    def step(fused_wo: bool):
+        x.copy_(x0)
+        for il, L in enumerate(layers):
+            ops.rms_norm(x, L["attn_norm"], 1e-5, out=cur)
+            ops.mul_mat_vec(L["wqkv"], cur, out=qkv)
+            kv.rope_append(il, q, k, v, seq1, pos1, pt, 1e6)
+            if fused_wo:
+                kv.decode_wo(il, q, pt, sl, ctx, L["wo"], x, y=ffn_inp)
+            else:
+                kv.decode(il, q, pt, sl, ctx, out=attn)
+                ops.mul_mat_vec(L["wo"], attn, residual=x, out=ffn_inp)
+            ops.rms_norm(ffn_inp, L["ffn_norm"], 1e-5, out=cur)
+            ops.moe_gate(L["gate_inp"], cur, K, ids=ids, weights=wts)
+            ops.moe_ffn(cur, ffn_inp, ids, wts, L["gate"], L["up"], L["down"], out=x, workspace=moe_ws)
+
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    res = {}
+    for fused in (True, False):
+        step(fused)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(3):
+            step(fused)
+        b.record()
+        torch.cuda.synchronize()
+        eager_us = a.elapsed_time(b) * 1e3 / (3 * n_layer)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(fused)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        res[fused] = (a.elapsed_time(b) * 1e3 / (steps * n_layer), eager_us)
+        del g
+    fused_best = res[True][0] <= res[False][0]
+    us, eager_us = res[fused_best]
+    out_ok = bool(torch.isfinite(x).all().item())
+    routed = ids.cpu().numpy().tolist()
+    alg = (2 * ((HQ + 2 * HKV) * HD * D + D * HQ * HD + E * D)      # Q/K/V, wo, router weights (f16)
+           + K * 3 * F * D * 2                                        # the routed experts' gate, up, down
+           + 2 * ctx * HKV * HD * 2                                   # K + V history (f16)
+           + 2 * D * 4)                                               # the two norm weights
+    ach = alg / (us * 1e-6) / 1e9
+    del layers, kv
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"whole decode layer on the GPU, Mixtral shape (n_embd 4096, 32q/8kv hd128, 8 experts "
+                    f"top-2, n_ff 14336), f16 weights, f16 KV at context 4096, B=1, {n_layer} layers with "
+                    f"distinct weights and caches, one HIP graph per token",
+        "us_per_layer_token": round(us, 2),
+        "us_per_layer_token_eager": round(eager_us, 2),
+        "tokens_per_s_32_layers": round(1e6 / (us * 32), 1),
+        "attention_wo": "sfa_attn_decode_wo (fused)" if fused_best else "sfa_attn_decode + sfa_mul_mat_vec(wo, residual)",
+        "us_per_layer_token_fused_wo": round(res[True][0], 2),
+        "us_per_layer_token_unfused_wo": round(res[False][0], 2),
+        "routed_experts_last_layer": routed,
+        "finite": out_ok,
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": alg,
+                     "kernel": "the layer's 12 launches (graph-replayed)",
+                     "what": "weights a layer-token reads (Q/K/V, wo, router, two experts) + KV history, once"},
+    }
 
 
 def f32_bench(torch, steps: int, warmup: int, seed: int):
@@ -848,7 +976,9 @@ def main():
     ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE + append leg")
     ap.add_argument("--no-f32", action="store_true", help="skip the F32-cache legs")
     ap.add_argument("--no-wo", action="store_true", help="skip the fused output-projection leg")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope", "f32", "wo"],
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-decode-layer leg")
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope", "f32", "wo",
+                                       "layer"],
                     help="run one leg only and print its JSON (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
@@ -878,7 +1008,7 @@ def main():
 
     if args.only == "decode4k":
         args.no_prefill = args.no_q8 = args.no_window = args.no_32k = args.no_cpu = args.no_rope = True
-        args.no_f32 = args.no_wo = True
+        args.no_f32 = args.no_wo = args.no_layer = True
     if args.only and args.only != "decode4k":
         if args.only == "decode32k":
             r = decode_leg(torch, "decode_f16_ctx32k", [32768], 1, max(args.steps // 4, 5), 3, args.seed + 4)
@@ -890,6 +1020,8 @@ def main():
             r = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
         elif args.only == "f32":
             r = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
+        elif args.only == "layer":
+            r = layer_bench(torch, max(args.steps // 5, 5), 2, args.seed + 8)
         elif args.only == "wo":
             r = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
         else:
@@ -959,6 +1091,8 @@ def main():
         result["f32"] = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
     if not args.no_wo:
         result["decode_wo"] = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
+    if not args.no_layer:
+        result["decode_layer"] = layer_bench(torch, max(args.steps // 5, 5), 2, args.seed + 8)
     result["hbm_copy_ceiling"] = copy_ceiling(torch)
     print(json.dumps(result))
 

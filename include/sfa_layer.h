@@ -14,6 +14,7 @@
  *   cur     = rms_norm(ffn_inp) * ffn_norm    sfa_rms_norm            engine.cpp:1908-1909
  *   logits  = gate_inp * cur                  sfa_mul_mat_vec         engine.cpp:1912
  *   ids, w  = top-k of softmax, renormalised  sfa_moe_route           engine.cpp:1913-1925
+ *             (both in one launch:            sfa_moe_gate)
  *   x'      = sum_j w_j * down_j(silu(gate_j * cur) * (up_j * cur)) + ffn_inp
  *                                             sfa_moe_ffn             engine.cpp:1964-1984
  *
@@ -58,6 +59,14 @@ SFA_API int sfa_mul_mat_vec(const void *w, int32_t w_type, const float *x, const
 SFA_API int sfa_moe_route(const float *logits, int32_t n_rows, int32_t n_expert, int32_t n_used,
                           int32_t *ids, float *weights, void *stream);
 
+/* The router product and the gating in one launch: logits = gate_inp * x
+ * (engine.cpp:1912, the sfa_mul_mat_vec arithmetic), then sfa_moe_route's
+ * selection and weights (engine.cpp:1913-1925).  gate_inp [n_expert][n_embd]
+ * f32 or f16, x [n_rows][n_embd] (n_embd a multiple of 8), n_expert <= 64. */
+SFA_API int sfa_moe_gate(const void *gate_inp, int32_t w_type, const float *x, int32_t n_rows,
+                         int32_t n_embd, int32_t n_expert, int32_t n_used, int32_t *ids,
+                         float *weights, void *stream);
+
 /* Workspace bytes of sfa_moe_ffn (the SwiGLU activations, n_rows * n_used *
  * n_ff floats); 0 for an invalid shape. */
 SFA_API size_t sfa_moe_workspace_bytes(int32_t n_rows, int32_t n_used, int32_t n_ff);
@@ -67,7 +76,8 @@ SFA_API size_t sfa_moe_workspace_bytes(int32_t n_rows, int32_t n_used, int32_t n
  *   act_j = silu(gate_exps[e] * x[t]) * (up_exps[e] * x[t])      (mul_mat_id, swiglu_split)
  *   y[t]  = sum over j in order of (down_exps[e] * act_j) * weights[t][j] + residual[t]
  * gate_exps / up_exps [n_expert][n_ff][n_embd], down_exps [n_expert][n_embd][n_ff],
- * all of w_type; n_embd and n_ff multiples of 8.  An id outside
+ * all of w_type; n_embd and n_ff multiples of 8, n_used <= 8 (else
+ * SFA_ERR_UNSUPPORTED).  An id outside
  * [0, n_expert) contributes nothing.  y must not alias x; it may alias
  * residual. */
 SFA_API int sfa_moe_ffn(const float *x, const float *residual, const int32_t *ids,

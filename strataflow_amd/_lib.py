@@ -50,6 +50,7 @@ LAYER_EXPORTS = (
     "sfa_rms_norm",
     "sfa_mul_mat_vec",
     "sfa_moe_route",
+    "sfa_moe_gate",
     "sfa_moe_workspace_bytes",
     "sfa_moe_ffn",
 )
@@ -139,6 +140,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_mul_mat_vec.restype = ctypes.c_int
     lib.sfa_moe_route.argtypes = [P, i32, i32, i32, P, P, P]
     lib.sfa_moe_route.restype = ctypes.c_int
+    lib.sfa_moe_gate.argtypes = [P, i32, P, i32, i32, i32, i32, P, P, P]
+    lib.sfa_moe_gate.restype = ctypes.c_int
     lib.sfa_moe_workspace_bytes.argtypes = [i32, i32, i32]
     lib.sfa_moe_workspace_bytes.restype = ctypes.c_size_t
     lib.sfa_moe_ffn.argtypes = [P, P, P, P, P, P, P, i32, i32, i32, i32, i32, i32, P, ctypes.c_size_t, P, P]

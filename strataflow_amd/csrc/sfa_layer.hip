@@ -65,25 +65,50 @@ __device__ inline float dot8(const floatx4 w0, const floatx4 w1, const floatx4 x
 // ---- rms_norm * weight --------------------------------------------------------
 
 // One workgroup per row: y = (x * (1/sqrtf(mean(x^2) + eps))) * w, the two
-// products rounded separately (ggml_rms_norm, then ggml_mul).
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const float *w, float *y, int n,
-                                                       float eps) {
-    __shared__ double part[kLayerWaves];
+// products rounded separately (ggml_rms_norm, then ggml_mul).  Up to
+// kNormRegs * 256 values per row are loaded (x and w) before any is used and
+// kept in registers, so the pass waits on memory once; longer rows loop over
+// the rest.
+constexpr int kNormThreads = 256;
+constexpr int kNormRegs = 16;
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *x, const float *w, float *y, int n,
+                                                                float eps) {
+    __shared__ double part[kNormThreads / 64];
     const float *xr = x + (int64_t)blockIdx.x * n;
     float *yr = y + (int64_t)blockIdx.x * n;
+    const int tid = threadIdx.x;
+    float xv[kNormRegs], wv[kNormRegs];
+#pragma unroll
+    for (int k = 0; k < kNormRegs; ++k) {
+        const int i = min(tid + kNormThreads * k, n - 1);  // clamped: every load in bounds
+        xv[k] = xr[i];
+        wv[k] = w[i];
+    }
     double s = 0.0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+#pragma unroll
+    for (int k = 0; k < kNormRegs; ++k) {
+        const float v = tid + kNormThreads * k < n ? xv[k] : 0.0f;
+        s += (double)(v * v);
+    }
+    for (int i = tid + kNormThreads * kNormRegs; i < n; i += kNormThreads) {
         const float v = xr[i];
         s += (double)(v * v);
     }
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    if ((tid & 63) == 0) part[tid >> 6] = s;
     __syncthreads();
     double t = 0.0;
-    for (int k = 0; k < (int)(blockDim.x >> 6); ++k) t += part[k];
+#pragma unroll
+    for (int k = 0; k < kNormThreads / 64; ++k) t += part[k];
     const float mean = (float)(t / n);
     const float scale = 1.0f / sqrtf(mean + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+#pragma unroll
+    for (int k = 0; k < kNormRegs; ++k) {
+        const int i = tid + kNormThreads * k;
+        if (i < n) yr[i] = __fmul_rn(__fmul_rn(xv[k], scale), wv[k]);
+    }
+    for (int i = tid + kNormThreads * kNormRegs; i < n; i += kNormThreads)
+        yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
 }
 
 // ---- mul_mat_vec ---------------------------------------------------------------
@@ -163,16 +188,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 
 // ---- routing --------------------------------------------------------------------
 
-// One wave per token, lane e holding expert e (n_expert <= 64): probabilities,
-// the n_used largest in descending order (ties: the lower expert first, a
-// stable descending argsort), their weights divided by their sum clamped at
-// 2^-14.
-__global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int n_expert, int n_used,
-                                                       int32_t *ids, float *weights) {
-    const int lane = threadIdx.x;
-    const float *lr = logits + (int64_t)blockIdx.x * n_expert;
+// Routing of one token by one wave, lane e holding logit e (n_expert <= 64):
+// probabilities, the n_used largest in descending order (ties: the lower
+// expert first, a stable descending argsort), their weights divided by their
+// sum clamped at 2^-14.
+__device__ inline void route_wave(float x, int lane, int n_expert, int n_used, int32_t *ids, float *weights) {
     const bool live = lane < n_expert;
-    const float x = live ? lr[lane] : -INFINITY;
+    x = live ? x : -INFINITY;
     const float mx = wave_max(x);
     const float e = live ? expf(x - mx) : 0.0f;
     double s = (double)e;
@@ -196,9 +218,60 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
     float sum = (float)ws;
     sum = sum < 6.103515625e-5f ? 6.103515625e-5f : sum;
     if (lane < n_used) {
-        ids[(int64_t)blockIdx.x * n_used + lane] = esel;
-        weights[(int64_t)blockIdx.x * n_used + lane] = __fdiv_rn(wsel, sum);
+        ids[lane] = esel;
+        weights[lane] = __fdiv_rn(wsel, sum);
     }
+}
+
+__global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int n_expert, int n_used,
+                                                       int32_t *ids, float *weights) {
+    const int lane = threadIdx.x;
+    const float x = logits[(int64_t)blockIdx.x * n_expert + min(lane, n_expert - 1)];
+    route_wave(x, lane, n_expert, n_used, ids + (int64_t)blockIdx.x * n_used,
+               weights + (int64_t)blockIdx.x * n_used);
+}
+
+// The router product and the routing in one launch (engine.cpp:1912-1925):
+// one workgroup per token; wave w computes the logits of experts w, w + 4, ..
+// (the mul_mat_vec arithmetic), wave 0 routes them from LDS.
+template <bool F16>
+__global__ __launch_bounds__(256) void moe_gate_kernel(const void *w, const float *x, int n_embd, int n_expert,
+                                                       int n_used, int32_t *ids, float *weights) {
+    __shared__ float lds_logit[64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int t = blockIdx.x;
+    const int nc = n_embd / 8;
+    const floatx4 *xr = reinterpret_cast<const floatx4 *>(x + (int64_t)t * n_embd);
+    for (int e0 = wave; e0 < n_expert; e0 += 2 * kLayerWaves) {
+        const int e1 = min(e0 + kLayerWaves, n_expert - 1);  // two rows per pass (clamped, stored once)
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+        for (int c = lane; c < nc; c += 64) {
+            if constexpr (F16) {
+                const half8 *W = static_cast<const half8 *>(w);
+                const half8 w0 = W[(int64_t)e0 * nc + c], w1 = W[(int64_t)e1 * nc + c];
+                const half8 xh = to_half8(xr[2 * c], xr[2 * c + 1]);
+                a0 = dot8(w0, xh, a0);
+                a1 = dot8(w1, xh, a1);
+            } else {
+                const floatx4 *W = static_cast<const floatx4 *>(w);
+                const floatx4 x0 = xr[2 * c], x1 = xr[2 * c + 1];
+                a0 = dot8(W[((int64_t)e0 * nc + c) * 2], W[((int64_t)e0 * nc + c) * 2 + 1], x0, x1, a0);
+                a1 = dot8(W[((int64_t)e1 * nc + c) * 2], W[((int64_t)e1 * nc + c) * 2 + 1], x0, x1, a1);
+            }
+        }
+        a0 = wave_sum(a0);
+        a1 = wave_sum(a1);
+        if (lane == 0) {
+            lds_logit[e0] = a0;
+            if (e0 + kLayerWaves < n_expert) lds_logit[e0 + kLayerWaves] = a1;
+        }
+    }
+    __syncthreads();
+    if (wave == 0)
+        route_wave(lds_logit[min(lane, n_expert - 1)], lane, n_expert, n_used, ids + (int64_t)t * n_used,
+                   weights + (int64_t)t * n_used);
 }
 
 // ---- experts --------------------------------------------------------------------
@@ -283,61 +356,76 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeParams p) {
 
 // y[t][o] = (sum over slots j in order of (down[e_j][o] . act[t][j]) * w[t][j])
 // + residual[t][o]; a slot with an id outside [0, n_expert) adds nothing.
-// Grid (row blocks of n_embd, n_rows).
-template <bool F16>
+// Every slot's rows stream in the same loop (NU slots, their loads in flight
+// together); two rows per wave, so a 4096-row output has 2048 waves.  Grid
+// (row blocks of n_embd, n_rows).
+constexpr int kDownRows = 2;
+template <bool F16, int NU>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int o0 = (int)blockIdx.x * kRowsPerBlock + wave * kRowsPerWave;
+    const int o0 = ((int)blockIdx.x * kLayerWaves + wave) * kDownRows;
     const int t = blockIdx.y;
     const int nc = p.n_ff / 8;
-    int rows[kRowsPerWave];
+    int rows[kDownRows];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) rows[r] = min(o0 + r, p.n_embd - 1);
-    float out[kRowsPerWave];
-    for (int j = 0; j < p.n_used; ++j) {
-        const int e_raw = p.ids[(int64_t)t * p.n_used + j];
-        const bool valid = e_raw >= 0 && e_raw < p.n_expert;
-        const int e = valid ? e_raw : 0;
-        const float wj = p.weights[(int64_t)t * p.n_used + j];
-        const floatx4 *ar = reinterpret_cast<const floatx4 *>(p.act + ((int64_t)t * p.n_used + j) * p.n_ff);
-        const int64_t mat = (int64_t)e * p.n_embd;
-        float d[kRowsPerWave];
+    for (int r = 0; r < kDownRows; ++r) rows[r] = min(o0 + r, p.n_embd - 1);
+    int64_t mat[NU];
+    bool valid[NU];
+    float wj[NU];
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) d[r] = 0.0f;
-#pragma unroll 4
-        for (int c = lane; c < nc; c += 64) {
+    for (int j = 0; j < NU; ++j) {
+        const int e_raw = p.ids[(int64_t)t * NU + j];
+        valid[j] = e_raw >= 0 && e_raw < p.n_expert;
+        mat[j] = (int64_t)(valid[j] ? e_raw : 0) * p.n_embd;
+        wj[j] = p.weights[(int64_t)t * NU + j];
+    }
+    const floatx4 *act = reinterpret_cast<const floatx4 *>(p.act + (int64_t)t * NU * p.n_ff);
+    float d[NU][kDownRows];
+#pragma unroll
+    for (int j = 0; j < NU; ++j)
+#pragma unroll
+        for (int r = 0; r < kDownRows; ++r) d[j][r] = 0.0f;
+#pragma unroll 2
+    for (int c = lane; c < nc; c += 64) {
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const floatx4 *ar = act + (int64_t)j * (p.n_ff / 4);
             if constexpr (F16) {
                 const half8 *D = static_cast<const half8 *>(p.down);
-                half8 dv[kRowsPerWave];
+                half8 dv[kDownRows];
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) dv[r] = D[(mat + rows[r]) * nc + c];
+                for (int r = 0; r < kDownRows; ++r) dv[r] = D[(mat[j] + rows[r]) * nc + c];
                 const half8 ah = to_half8(ar[2 * c], ar[2 * c + 1]);
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) d[r] = dot8(dv[r], ah, d[r]);
+                for (int r = 0; r < kDownRows; ++r) d[j][r] = dot8(dv[r], ah, d[j][r]);
             } else {
                 const floatx4 *D = static_cast<const floatx4 *>(p.down);
-                floatx4 d0[kRowsPerWave], d1[kRowsPerWave];
+                floatx4 d0[kDownRows], d1[kDownRows];
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) {
-                    d0[r] = D[((mat + rows[r]) * nc + c) * 2];
-                    d1[r] = D[((mat + rows[r]) * nc + c) * 2 + 1];
+                for (int r = 0; r < kDownRows; ++r) {
+                    d0[r] = D[((mat[j] + rows[r]) * nc + c) * 2];
+                    d1[r] = D[((mat[j] + rows[r]) * nc + c) * 2 + 1];
                 }
                 const floatx4 a0 = ar[2 * c], a1 = ar[2 * c + 1];
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) d[r] = dot8(d0[r], d1[r], a0, a1, d[r]);
+                for (int r = 0; r < kDownRows; ++r) d[j][r] = dot8(d0[r], d1[r], a0, a1, d[j][r]);
             }
         }
+    }
+    float out[kDownRows];
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
-            const float v = valid ? __fmul_rn(wave_sum(d[r]), wj) : 0.0f;
+    for (int r = 0; r < kDownRows; ++r) {
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const float v = valid[j] ? __fmul_rn(wave_sum(d[j][r]), wj[j]) : 0.0f;
             out[r] = j == 0 ? v : __fadd_rn(out[r], v);
         }
     }
-    if (lane < kRowsPerWave && o0 + lane < p.n_embd) {
+    if (lane < kDownRows && o0 + lane < p.n_embd) {
         float v = out[0];
 #pragma unroll
-        for (int r = 1; r < kRowsPerWave; ++r) v = lane == r ? out[r] : v;
+        for (int r = 1; r < kDownRows; ++r) v = lane == r ? out[r] : v;
         const int64_t o = (int64_t)t * p.n_embd + o0 + lane;
         p.y[o] = __fadd_rn(v, p.residual[o]);
     }
@@ -377,7 +465,8 @@ SFA_API int sfa_rms_norm(const float *x, const float *weight, float *y, int32_t 
         if (x == nullptr || weight == nullptr || y == nullptr) return SFA_ERR_INVALID_ARGUMENT;
         if (n_rows < 0 || n_embd <= 0 || !(eps >= 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
         if (n_rows == 0) return SFA_OK;
-        hipLaunchKernelGGL(sfa::rms_norm_kernel, dim3(n_rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+        hipLaunchKernelGGL(sfa::rms_norm_kernel, dim3(n_rows), dim3(sfa::kNormThreads), 0,
+                           static_cast<hipStream_t>(stream),
                            x, weight, y, n_embd, eps);
         return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
     } catch (...) {
@@ -415,6 +504,28 @@ SFA_API int sfa_moe_route(const float *logits, int32_t n_rows, int32_t n_expert,
     }
 }
 
+SFA_API int sfa_moe_gate(const void *gate_inp, int32_t w_type, const float *x, int32_t n_rows, int32_t n_embd,
+                         int32_t n_expert, int32_t n_used, int32_t *ids, float *weights, void *stream) {
+    try {
+        if (gate_inp == nullptr || x == nullptr || ids == nullptr || weights == nullptr)
+            return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows < 0 || n_embd <= 0 || n_expert <= 0 || n_used <= 0 || n_used > n_expert)
+            return SFA_ERR_INVALID_ARGUMENT;
+        if (!sfa::weight_type_ok(w_type) || n_embd % 8 != 0 || n_expert > 64) return SFA_ERR_UNSUPPORTED;
+        if (n_rows == 0) return SFA_OK;
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        if (w_type == SFA_KV_F16)
+            hipLaunchKernelGGL(sfa::moe_gate_kernel<true>, dim3(n_rows), dim3(256), 0, s, gate_inp, x, n_embd,
+                               n_expert, n_used, ids, weights);
+        else
+            hipLaunchKernelGGL(sfa::moe_gate_kernel<false>, dim3(n_rows), dim3(256), 0, s, gate_inp, x, n_embd,
+                               n_expert, n_used, ids, weights);
+        return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
 SFA_API size_t sfa_moe_workspace_bytes(int32_t n_rows, int32_t n_used, int32_t n_ff) {
     if (n_rows <= 0 || n_used <= 0 || n_ff <= 0) return 0;
     return (size_t)n_rows * n_used * n_ff * sizeof(float);
@@ -434,18 +545,32 @@ SFA_API int sfa_moe_ffn(const float *x, const float *residual, const int32_t *id
         if (n_rows == 0) return SFA_OK;
         if (workspace == nullptr || ws_bytes < sfa_moe_workspace_bytes(n_rows, n_used, n_ff))
             return SFA_ERR_INVALID_ARGUMENT;
-        if (n_rows > 65535 || n_used > 65535) return SFA_ERR_UNSUPPORTED;
+        if (n_rows > 65535 || n_used > 8) return SFA_ERR_UNSUPPORTED;
         sfa::MoeParams p{x, residual, ids, weights, gate_exps, up_exps, down_exps, static_cast<float *>(workspace),
                          y, n_rows, n_embd, n_ff, n_expert, n_used};
         const hipStream_t s = static_cast<hipStream_t>(stream);
         const bool f16 = w_type == SFA_KV_F16;
-        const dim3 g1(sfa::grid_x(n_ff), n_used, n_rows), g2(sfa::grid_x(n_embd), n_rows);
-        if (f16) {
+        const dim3 g1(sfa::grid_x(n_ff), n_used, n_rows);
+        const dim3 g2((n_embd + sfa::kLayerWaves * sfa::kDownRows - 1) / (sfa::kLayerWaves * sfa::kDownRows), n_rows);
+        if (f16)
             hipLaunchKernelGGL(sfa::moe_gate_up_kernel<true>, g1, dim3(256), 0, s, p);
-            hipLaunchKernelGGL(sfa::moe_down_kernel<true>, g2, dim3(256), 0, s, p);
-        } else {
+        else
             hipLaunchKernelGGL(sfa::moe_gate_up_kernel<false>, g1, dim3(256), 0, s, p);
-            hipLaunchKernelGGL(sfa::moe_down_kernel<false>, g2, dim3(256), 0, s, p);
+        switch (n_used) {
+#define SFA_DOWN(NU)                                                                       \
+    case NU:                                                                               \
+        if (f16) hipLaunchKernelGGL((sfa::moe_down_kernel<true, NU>), g2, dim3(256), 0, s, p);   \
+        else hipLaunchKernelGGL((sfa::moe_down_kernel<false, NU>), g2, dim3(256), 0, s, p);      \
+        break;
+            SFA_DOWN(1)
+            SFA_DOWN(2)
+            SFA_DOWN(3)
+            SFA_DOWN(4)
+            SFA_DOWN(5)
+            SFA_DOWN(6)
+            SFA_DOWN(7)
+            SFA_DOWN(8)
+#undef SFA_DOWN
         }
         return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
     } catch (...) {

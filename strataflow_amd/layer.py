@@ -14,7 +14,7 @@ import torch
 from . import _lib
 from ._lib import SFA_KV_F16, SFA_KV_F32
 
-__all__ = ["rms_norm", "mul_mat_vec", "moe_route", "moe_ffn", "weight_type"]
+__all__ = ["rms_norm", "mul_mat_vec", "moe_route", "moe_gate", "moe_ffn", "weight_type"]
 
 
 def _stream(stream) -> int:
@@ -77,6 +77,24 @@ def moe_route(logits: torch.Tensor, n_used: int, ids: torch.Tensor | None = None
         weights = torch.empty((n_rows, n_used), dtype=torch.float32, device=logits.device)
     _lib.check(_lib.load().sfa_moe_route(logits.data_ptr(), n_rows, n_expert, n_used, ids.data_ptr(),
                                          weights.data_ptr(), _stream(stream)), "sfa_moe_route")
+    return ids, weights
+
+
+def moe_gate(gate_inp: torch.Tensor, x: torch.Tensor, n_used: int, ids: torch.Tensor | None = None,
+             weights: torch.Tensor | None = None, stream=None):
+    """The router product and the routing in one launch: x [n_rows, n_embd],
+    gate_inp [n_expert, n_embd] -> (ids int32, weights f32) [n_rows, n_used]."""
+    _f32(x, "x")
+    n_rows, n_embd = x.shape
+    n_expert = gate_inp.shape[0]
+    assert gate_inp.is_contiguous() and gate_inp.shape == (n_expert, n_embd)
+    if ids is None:
+        ids = torch.empty((n_rows, n_used), dtype=torch.int32, device=x.device)
+    if weights is None:
+        weights = torch.empty((n_rows, n_used), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.load().sfa_moe_gate(gate_inp.data_ptr(), weight_type(gate_inp), x.data_ptr(), n_rows, n_embd,
+                                        n_expert, n_used, ids.data_ptr(), weights.data_ptr(), _stream(stream)),
+               "sfa_moe_gate")
     return ids, weights
 
 

@@ -265,7 +265,7 @@ class TinyMoeGpu(TinyMoe):
                 attn = self.kv.prefill(il, q, self.pt[0], pos0)
                 ffn_inp = ops.mul_mat_vec(L["wo"], attn, residual=x)
             cur = ops.rms_norm(ffn_inp, L["ffn_norm"], cfg.rms_eps)
-            ids, wts = ops.moe_route(ops.mul_mat_vec(L["gate_inp"], cur), cfg.n_expert_used)
+            ids, wts = ops.moe_gate(L["gate_inp"], cur, cfg.n_expert_used)
             need = T * cfg.n_expert_used * cfg.n_ff * 4
             if self._moe_ws is None or self._moe_ws.numel() < need:
                 self._moe_ws = torch.empty(need, dtype=torch.uint8, device=dev)

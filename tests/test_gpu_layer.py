@@ -222,3 +222,23 @@ def test_layer_ops_in_a_graph(gpu):
         step()
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int32), y.view(torch.int32)), s
+
+
+@pytest.mark.parametrize("wdtype", ["f32", "f16"])
+@pytest.mark.parametrize("n_rows,n_embd,n_expert,k", [(1, 4096, 8, 2), (3, 256, 8, 2), (2, 512, 64, 6), (1, 128, 3, 3)])
+def test_moe_gate_equals_product_then_route(gpu, wdtype, n_rows, n_embd, n_expert, k):
+    """The fused router product + routing gives the bits of sfa_mul_mat_vec then
+    sfa_moe_route (the same dot arithmetic)."""
+    from strataflow_amd import layer
+    rng = np.random.default_rng(n_embd + n_expert)
+    w = (rng.standard_normal((n_expert, n_embd)) / np.sqrt(n_embd)).astype(np.float32)
+    if wdtype == "f16":
+        w = w.astype(np.float16)
+    x = rng.standard_normal((n_rows, n_embd)).astype(np.float32)
+    tw, tx = _t(w, gpu), _t(x, gpu)
+    ids, wts = layer.moe_gate(tw, tx, k)
+    ids2, wts2 = layer.moe_route(layer.mul_mat_vec(tw, tx), k)
+    assert np.array_equal(ids.cpu().numpy(), ids2.cpu().numpy())
+    assert np.array_equal(wts.cpu().numpy().view(np.uint32), wts2.cpu().numpy().view(np.uint32))
+    sel, _ = _route_ref(_mm_ref(w, x, wdtype == "f16").astype(np.float32), k)
+    assert np.array_equal(ids.cpu().numpy(), sel)
