@@ -582,7 +582,7 @@ def layer_bench(torch, steps: int, warmup: int, seed: int, n_layer: int = 8) -> 
         "finite": out_ok,
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": alg,
-                     "kernel": "the layer's 12 launches (graph-replayed)",
+                     "kernel": "the layer's launches (graph-replayed)",
                      "what": "weights a layer-token reads (Q/K/V, wo, router, two experts) + KV history, once"},
     }
 

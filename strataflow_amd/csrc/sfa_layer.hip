@@ -18,9 +18,9 @@
 // multiplied by their weights, added in slot order, then the residual is added.
 //
 // Every kernel is HBM-bound at decode (one or a few tokens per weight read):
-// a wave owns four output rows and its lanes stream each row in 16-byte
-// chunks, so one wave keeps 4 rows x 4 chunks x 1 KB in flight; activations
-// (a few KB) come from L2.  Weights are row-major [n_out][n_in] (ggml ne =
+// a wave owns one to four output rows and its lanes stream each row in
+// 16-byte chunks, several chunks in flight per lane; activations (a few KB)
+// come from L2.  Weights are row-major [n_out][n_in] (ggml ne =
 // [n_in, n_out]); expert stacks are [n_expert][n_out][n_in].
 #include <exception>
 
@@ -31,7 +31,7 @@ namespace sfa {
 
 constexpr int kRowsPerWave = 4;
 constexpr int kLayerWaves = 4;
-constexpr int kRowsPerBlock = kRowsPerWave * kLayerWaves;
+constexpr int kRowsPerBlock = kRowsPerWave * kLayerWaves;  // expert gate/up rows per workgroup
 
 // 8 consecutive activations as the f16 operand of F16 weights (RNE, the
 // FP32 -> FP16 conversion ggml applies to src1)
@@ -121,46 +121,50 @@ struct GemvParams {
     int n_rows, n_in, n_out;
 };
 
-// Wave w of block b owns rows 16b + 4w .. +3 (clamped to n_out - 1 for the
-// loads, not stored) for NT tokens starting at token blockIdx.y * NT.
-template <bool F16, int NT>
+// Wave w of block b owns rows RW * (4b + w) .. + RW - 1 (clamped to n_out - 1
+// for the loads, not stored) for NT tokens starting at token blockIdx.y * NT.
+// RW follows n_out so that a launch has about 4096 waves or more: one row per
+// wave for the 4096- and 6144-row products of a decode layer (every chunk of
+// a row in flight at once), four for wide ones.
+template <bool F16, int NT, int RW>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row0 = (int)blockIdx.x * kRowsPerBlock + wave * kRowsPerWave;
+    const int row0 = ((int)blockIdx.x * kLayerWaves + wave) * RW;
     const int tok0 = (int)blockIdx.y * NT;
     const int nc = p.n_in / 8;  // 8-element chunks per row
-    float acc[kRowsPerWave][NT];
+    float acc[RW][NT];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r)
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[r][t] = 0.0f;
-    int rows[kRowsPerWave];
+    int rows[RW];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) rows[r] = min(row0 + r, p.n_out - 1);
+    for (int r = 0; r < RW; ++r) rows[r] = min(row0 + r, p.n_out - 1);
     int toks[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) toks[t] = min(tok0 + t, p.n_rows - 1);
 
-#pragma unroll 4
+    constexpr int kUnroll = RW == 1 ? 8 : 4;
+#pragma unroll kUnroll
     for (int c = lane; c < nc; c += 64) {
         if constexpr (F16) {
             const half8 *W = static_cast<const half8 *>(p.w);
-            half8 wv[kRowsPerWave];
+            half8 wv[RW];
 #pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) wv[r] = W[(int64_t)rows[r] * nc + c];
+            for (int r = 0; r < RW; ++r) wv[r] = W[(int64_t)rows[r] * nc + c];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)toks[t] * p.n_in) + 2 * c;
                 const half8 xh = to_half8(xr[0], xr[1]);
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) acc[r][t] = dot8(wv[r], xh, acc[r][t]);
+                for (int r = 0; r < RW; ++r) acc[r][t] = dot8(wv[r], xh, acc[r][t]);
             }
         } else {
             const floatx4 *W = static_cast<const floatx4 *>(p.w);
-            floatx4 w0[kRowsPerWave], w1[kRowsPerWave];
+            floatx4 w0[RW], w1[RW];
 #pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) {
+            for (int r = 0; r < RW; ++r) {
                 w0[r] = W[((int64_t)rows[r] * nc + c) * 2];
                 w1[r] = W[((int64_t)rows[r] * nc + c) * 2 + 1];
             }
@@ -169,12 +173,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
                 const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)toks[t] * p.n_in) + 2 * c;
                 const floatx4 x0 = xr[0], x1 = xr[1];
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) acc[r][t] = dot8(w0[r], w1[r], x0, x1, acc[r][t]);
+                for (int r = 0; r < RW; ++r) acc[r][t] = dot8(w0[r], w1[r], x0, x1, acc[r][t]);
             }
         }
     }
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) {
+    for (int r = 0; r < RW; ++r) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const float v = wave_sum(acc[r][t]);
@@ -435,13 +439,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
 
 static int grid_x(int n) { return (n + kRowsPerBlock - 1) / kRowsPerBlock; }
 
-static int gemv_launch(const GemvParams &p, bool f16, hipStream_t s) {
-    const int nt = p.n_rows >= 8 ? 8 : p.n_rows >= 4 ? 4 : p.n_rows >= 2 ? 2 : 1;
-    const dim3 grid(grid_x(p.n_out), (p.n_rows + nt - 1) / nt);
-#define SFA_GEMV(NT)                                                                        \
-    case NT:                                                                                \
-        if (f16) hipLaunchKernelGGL((gemv_kernel<true, NT>), grid, dim3(256), 0, s, p);    \
-        else hipLaunchKernelGGL((gemv_kernel<false, NT>), grid, dim3(256), 0, s, p);       \
+template <int RW>
+static void gemv_launch_rw(const GemvParams &p, bool f16, int nt, hipStream_t s) {
+    const dim3 grid((p.n_out + kLayerWaves * RW - 1) / (kLayerWaves * RW), (p.n_rows + nt - 1) / nt);
+#define SFA_GEMV(NT)                                                                           \
+    case NT:                                                                                   \
+        if (f16) hipLaunchKernelGGL((gemv_kernel<true, NT, RW>), grid, dim3(256), 0, s, p);   \
+        else hipLaunchKernelGGL((gemv_kernel<false, NT, RW>), grid, dim3(256), 0, s, p);      \
         break;
     switch (nt) {
         SFA_GEMV(1)
@@ -450,6 +454,16 @@ static int gemv_launch(const GemvParams &p, bool f16, hipStream_t s) {
         SFA_GEMV(8)
     }
 #undef SFA_GEMV
+}
+
+static int gemv_launch(const GemvParams &p, bool f16, hipStream_t s) {
+    const int nt = p.n_rows >= 8 ? 8 : p.n_rows >= 4 ? 4 : p.n_rows >= 2 ? 2 : 1;
+    if (p.n_out >= 16384)
+        gemv_launch_rw<4>(p, f16, nt, s);
+    else if (p.n_out >= 8192)
+        gemv_launch_rw<2>(p, f16, nt, s);
+    else
+        gemv_launch_rw<1>(p, f16, nt, s);
     return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
 }
 
