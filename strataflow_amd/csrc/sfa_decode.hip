@@ -1171,11 +1171,15 @@ void decode_q8_kernel(DecodeParams p) {
 // clamped (the loads stay inside the workspace) and their weights are zero.
 // A batch sequence without tiles gets a zero output here.  The code is
 // branch-free straight-line work: the pass is latency-bound and each taken
-// branch or instruction-cache miss adds to it.
-template <int HD, int G, bool ONE>
+// branch or instruction-cache miss adds to it.  CH partial rows are loaded
+// per round: 32 when the row has at most 32 slots (one round, no duplicate
+// loads) else 64; the (m, l) of split s sit in lane s % 64 of register s / 64
+// (one register for a row of at most 32 slots).
+template <int HD, int G, bool ONE, int CH>
 __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeParams p) {
-    constexpr int CH = kWave;                       // splits per round
-    constexpr int RMAX = (kMaxSplits + CH - 1) / CH;  // (m, l) registers per lane
+    static_assert(CH == 32 || CH == 64, "round size");
+    // (m, l) registers per lane: one when the row has at most 32 slots
+    constexpr int RMAX = CH == 32 ? 1 : (kMaxSplits + kWave - 1) / kWave;
     const int g = blockIdx.x % G;
     const int kvh = (blockIdx.x / G) % p.n_head_kv;
     const int b = blockIdx.x / (G * p.n_head_kv);
@@ -1196,7 +1200,7 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     auto load_ml = [&](const float *pg, int S) {
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
-            const int s = min(CH * r + lane, S - 1);
+            const int s = min(kWave * r + lane, S - 1);
             mv[r] = pg[(int64_t)s * sstride + HD];
             lv[r] = pg[(int64_t)s * sstride + HD + 1];
         }
@@ -1235,7 +1239,7 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
-        mv[r] = CH * r + lane < n_active ? mv[r] : -INFINITY;
+        mv[r] = kWave * r + lane < n_active ? mv[r] : -INFINITY;
         mx = fmaxf(mx, mv[r]);
     }
     const float M = wave_max(mx);
@@ -1251,12 +1255,13 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     // is zero and their (possibly stale) values are never multiplied
     float O = 0.0f;
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
+    for (int r = 0; r < kMaxSplits / CH; ++r) {
         if (CH * r >= n_active) break;
         if (r > 0) load_round(pg, CH * r, S);
 #pragma unroll
         for (int u = 0; u < CH; ++u) {
-            const float wt = lane_val(w[r], u);
+            const int sp = CH * r + u;  // compile-time
+            const float wt = lane_val(w[sp / kWave], sp % kWave);
             O = wt != 0.0f ? fmaf(o[u], wt, O) : O;
         }
     }
@@ -1328,12 +1333,22 @@ size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
 template <int HD, int G>
 static void launch_merge(const DecodeParams &p, int B, int Hkv, int passes, hipStream_t s) {
     if ((passes & 2) && !p.one_split) {
-        if (B == 1)
-            hipLaunchKernelGGL((decode_merge_kernel<HD, G, true>), dim3(Hkv * G), dim3(kMergeThreads<HD>), 0,
-                               s, p);
-        else
-            hipLaunchKernelGGL((decode_merge_kernel<HD, G, false>), dim3(B * Hkv * G),
-                               dim3(kMergeThreads<HD>), 0, s, p);
+        const bool small = p.split_row <= 32;
+        if (B == 1) {
+            if (small)
+                hipLaunchKernelGGL((decode_merge_kernel<HD, G, true, 32>), dim3(Hkv * G), dim3(kMergeThreads<HD>),
+                                   0, s, p);
+            else
+                hipLaunchKernelGGL((decode_merge_kernel<HD, G, true, 64>), dim3(Hkv * G), dim3(kMergeThreads<HD>),
+                                   0, s, p);
+        } else {
+            if (small)
+                hipLaunchKernelGGL((decode_merge_kernel<HD, G, false, 32>), dim3(B * Hkv * G),
+                                   dim3(kMergeThreads<HD>), 0, s, p);
+            else
+                hipLaunchKernelGGL((decode_merge_kernel<HD, G, false, 64>), dim3(B * Hkv * G),
+                                   dim3(kMergeThreads<HD>), 0, s, p);
+        }
     }
 }
 
