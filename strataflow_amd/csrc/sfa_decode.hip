@@ -717,27 +717,33 @@ void decode_q8_kernel(DecodeParams p) {
     uint8_t *vt = lds_v[wave];
     const int wave_u = __builtin_amdgcn_readfirstlane(COLS ? 0 : wave);
 
-    // K operand of block c for lane (row n, half hh): quants 16hh..16hh+15 of
-    // block c and the block scale; V: blocks VBL*hh .. of row n.  All kept
-    // as loaded (arithmetic on them at issue time would make the wave wait
-    // for the prefetched tile right where it issues it); the byte alignment
-    // of even K blocks happens when the tile is consumed.  Two such register
-    // sets (tiles A and B) alternate: the loop is unrolled by two so each set
-    // is loaded and consumed in place, never copied (a copy of a register
-    // still being loaded would wait for the load).
+    // Lane (row n, half hh) loads one contiguous, 4-aligned piece of row n of
+    // K and of V: head_dim 128, bytes 68hh .. 68hh + 67 (blocks 2hh and
+    // 2hh + 1, 17 dwords); head_dim 64, bytes 32hh .. 32hh + 35 (block hh
+    // and two bytes beside it, 9 dwords): five (three) loads per row and
+    // tensor.  The V blocks are the ones the lane dequantises; the K operand
+    // of block c (quants 16hh .. 16hh + 15) is put together when the tile is
+    // consumed, the halves trading their quants across the 32-lane boundary
+    // (v_permlane32_swap).  All kept as loaded (arithmetic on them at issue
+    // time would make the wave wait for the prefetched tile right where it
+    // issues it).  Two such register sets (tiles A and B) alternate: the loop
+    // is unrolled by two so each set is loaded and consumed in place, never
+    // copied (a copy of a register still being loaded would wait for the
+    // load).
+    constexpr int KQ = HD / 32;          // 16-byte loads per piece
     struct Raw {
-        intx4 kw[NB];                // 16 bytes at 34c + 16hh (c even) or 34c + 2 + 16hh (c odd)
-        uint32_t kx[NB / 2 > 0 ? NB / 2 : 1];  // the dword after them (even c)
-        uint32_t kd[NB];             // dword holding d_k of block c
-        uint32_t vw[VBL][9];         // the 36 bytes around each V block
+        intx4 k4[KQ];
+        uint32_t k1;
+        intx4 v4[KQ];
+        uint32_t v1;
     };
     PageWindow pages;
     // Tile t's loads (page id pid, wave-uniform) are buffer loads over the
     // kv head's rows of the tile, issued unconditionally: an invalid page gets
     // a zero-byte descriptor (loads return zeros, nothing is read) and false.
     // Every offset is 4-byte aligned (rows are 136 or 68 bytes, columns a
-    // multiple of 4, blocks at 34c or 34c + 2 as below).
-    const int row_lane = n * (int)col_bytes;
+    // multiple of 4, pieces at 68hh or 32hh).
+    const int row_lane = n * (int)col_bytes + (HD == 128 ? 68 : 32) * hh;
     auto issue = [&](int t, Raw &r, int32_t pid) -> bool {
         const int pos0 = t * kTile;
         const int lpage = pos0 / p.page_size;
@@ -753,26 +759,11 @@ void decode_q8_kernel(DecodeParams p) {
             const uint8_t *kr = kb + off + row_lane;
             const uint8_t *vr = vb + off + row_lane;
 #pragma unroll
-            for (int c = 0; c < NB; ++c) {
-                if ((c & 1) == 0) {
-                    const uint8_t *w = kr + 34 * c + 16 * hh;
-                    r.kw[c] = load16_a4(w);
-                    r.kx[c / 2] = load4_a4(w + 16);
-                    r.kd[c] = load4_a4(kr + 34 * c);
-                } else {
-                    r.kw[c] = load16_a4(kr + 34 * c + 2 + 16 * hh);
-                    r.kd[c] = load4_a4(kr + 34 * c - 2);
-                }
-            }
+            for (int j = 0; j < KQ; ++j) r.k4[j] = load16_a4(kr + 16 * j);
+            r.k1 = load4_a4(kr + 16 * KQ);
 #pragma unroll
-            for (int u = 0; u < VBL; ++u) {
-                const int c = VBL * hh + u;
-                const uint8_t *w = vr + 34 * c - (c & 1) * 2;
-                const intx4 a0 = load16_a4(w), a1 = load16_a4(w + 16);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) { r.vw[u][j] = (uint32_t)a0[j]; r.vw[u][4 + j] = (uint32_t)a1[j]; }
-                r.vw[u][8] = load4_a4(w + 32);
-            }
+            for (int j = 0; j < KQ; ++j) r.v4[j] = load16_a4(vr + 16 * j);
+            r.v1 = load4_a4(vr + 16 * KQ);
             return true;
         }
         const int n_rec = ok ? (kTile - 1) * (int)col_bytes + p.row_bytes : 0;
@@ -787,30 +778,11 @@ void decode_q8_kernel(DecodeParams p) {
             return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, row_lane + o, 0, 0);
         };
 #pragma unroll
-        for (int c = 0; c < NB; ++c) {
-            if ((c & 1) == 0) {
-                // block at 34c (4-aligned): quants of half hh start 2 bytes
-                // into the dword at 34c + 16hh; d is the low half at 34c
-                r.kw[c] = ld16(rk, 34 * c + 16 * hh);
-                r.kx[c / 2] = ld4(rk, 34 * c + 16 * hh + 16);
-                r.kd[c] = ld4(rk, 34 * c);
-            } else {
-                // block at 34c (2 mod 4): quants 4-aligned; d is the high half
-                // of the dword at 34c - 2
-                r.kw[c] = ld16(rk, 34 * c + 2 + 16 * hh);
-                r.kd[c] = ld4(rk, 34 * c - 2);
-            }
-        }
+        for (int j = 0; j < KQ; ++j) r.k4[j] = ld16(rk, 16 * j);
+        r.k1 = ld4(rk, 16 * KQ);
 #pragma unroll
-        for (int u = 0; u < VBL; ++u) {
-            const int c = VBL * hh + u;
-            // 9 dwords from the 4-aligned offset at or 2 bytes below the block
-            const int w = 34 * c - (c & 1) * 2;
-            const intx4 a0 = ld16(rv, w), a1 = ld16(rv, w + 16);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { r.vw[u][j] = (uint32_t)a0[j]; r.vw[u][4 + j] = (uint32_t)a1[j]; }
-            r.vw[u][8] = ld4(rv, w + 32);
-        }
+        for (int j = 0; j < KQ; ++j) r.v4[j] = ld16(rv, 16 * j);
+        r.v1 = ld4(rv, 16 * KQ);
         return ok;
     };
     auto page_of = [&](int t) -> int32_t {
@@ -940,41 +912,95 @@ void decode_q8_kernel(DecodeParams p) {
         const int pos0 = t * kTile;
         const bool row_ok = pos0 + n >= lo && pos0 + n < n_kv;
         const bool interior = pos0 >= lo && pos0 + kTile <= n_kv;
+        // K operands.  Half-row dwords D (local byte 0 = row byte 68hh or
+        // 32hh).  head_dim 128: the half's first block (2hh) has d at local
+        // bytes 0-1 and quants 0-15 / 16-31 at 2-17 / 18-33, its second
+        // (2hh + 1) d at 34-35 and quants at 36-51 / 52-67 (dwords 9-12 /
+        // 13-16).  head_dim 64: half 0 holds block 0 as the first block
+        // above; half 1 (from row byte 32) block 1 with d at local 2-3 and
+        // quants at dwords 1-4 / 5-8.  Per pair of blocks the lane forms X =
+        // its block's quants 0-15 and Y = quants 16-31; swapping X's upper 32
+        // lanes with Y's lower 32 leaves X = the first block of half 0 (lanes
+        // of half hh holding quants 16hh ..) and Y = that of half 1.
+        intx4 kop[NB];
+        uint32_t kdb[NB];
+        {
+            uint32_t D[4 * KQ + 1];
+#pragma unroll
+            for (int j = 0; j < KQ; ++j) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) D[4 * j + e] = (uint32_t)r.k4[j][e];
+            }
+            D[4 * KQ] = r.k1;
+            // bytes 2.. of dwords j, j+1 (head_dim 128, and half 0 of 64);
+            // dword j + 1 itself for half 1 of head_dim 64
+            const uint32_t sel = (HD == 64 && hh) ? 0x07060504u : 0x05040302u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t x = __builtin_amdgcn_perm(D[j + 1], D[j], sel);
+                const uint32_t y = __builtin_amdgcn_perm(D[j + 5], D[j + 4], sel);
+                const auto s = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+                kop[0][j] = (int)s[0];
+                kop[NB / 2][j] = (int)s[1];
+            }
+            if constexpr (HD == 128) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const auto s = __builtin_amdgcn_permlane32_swap(D[9 + j], D[13 + j], false, false);
+                    kop[1][j] = (int)s[0];
+                    kop[3][j] = (int)s[1];
+                }
+                // d of the half's two blocks (low half of dword 0, high half
+                // of dword 8), then both halves' pairs to every lane
+                const uint32_t dd = __builtin_amdgcn_perm(D[8], D[0], 0x07060100u);
+                const auto s = __builtin_amdgcn_permlane32_swap(dd, dd, false, false);
+                kdb[0] = s[0] & 0xffffu;
+                kdb[1] = s[0] >> 16;
+                kdb[2] = s[1] & 0xffffu;
+                kdb[3] = s[1] >> 16;
+            } else {
+                const uint32_t dd = hh ? D[0] >> 16 : D[0] & 0xffffu;
+                const auto s = __builtin_amdgcn_permlane32_swap(dd, dd, false, false);
+                kdb[0] = s[0];
+                kdb[1] = s[1];
+            }
+        }
         // S = Q8 * K8^T per block, scaled in block order
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = 0.0f;
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
-            intx4 kq = r.kw[c];
-            if ((c & 1) == 0) {
-                const uint32_t *x = reinterpret_cast<const uint32_t *>(&r.kw[c]);
-                kq[0] = (int)__builtin_amdgcn_alignbyte(x[1], x[0], 2);
-                kq[1] = (int)__builtin_amdgcn_alignbyte(x[2], x[1], 2);
-                kq[2] = (int)__builtin_amdgcn_alignbyte(x[3], x[2], 2);
-                kq[3] = (int)__builtin_amdgcn_alignbyte(r.kx[c / 2], x[3], 2);
-            }
-            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lds_qa[qw][n % G][c][hh], kq, intx16{}, 0, 0, 0);
-            const uint32_t dbits = (c & 1) ? (r.kd[c] >> 16) : (r.kd[c] & 0xffffu);
-            const float dk = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
+            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lds_qa[qw][n % G][c][hh], kop[c], intx16{}, 0, 0, 0);
+            const float dk = (float)__builtin_bit_cast(_Float16, (uint16_t)kdb[c]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) sv[i] += (float)acc[i] * (dk * lds_dq[qw][(4 * hh + i) % G][c]);
             // one block's 16-register accumulator live at a time
             __builtin_amdgcn_sched_barrier(0);
         }
-        // V blocks: dequantise into the f16 LDS tile (rows outside [lo, n_kv) zeroed)
+        // V blocks: dequantise into the f16 LDS tile (rows outside [lo, n_kv)
+        // zeroed).  Block u of the lane's piece spans dwords 8u .. 8u + 8;
+        // an even block has d at the low half of its first dword.
+        uint32_t Dv[4 * KQ + 1];
+#pragma unroll
+        for (int j = 0; j < KQ; ++j) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Dv[4 * j + e] = (uint32_t)r.v4[j][e];
+        }
+        Dv[4 * KQ] = r.v1;
 #pragma unroll
         for (int u = 0; u < VBL; ++u) {
             const int c = VBL * hh + u;
+            const uint32_t *w = Dv + 8 * u;
             uint32_t q[8];
             uint32_t dbits;
             if ((c & 1) == 0) {
-                dbits = r.vw[u][0] & 0xffffu;
+                dbits = w[0] & 0xffffu;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(r.vw[u][j + 1], r.vw[u][j], 2);
+                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], 2);
             } else {
-                dbits = r.vw[u][0] >> 16;
+                dbits = w[0] >> 16;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = r.vw[u][j + 1];
+                for (int j = 0; j < 8; ++j) q[j] = w[j + 1];
             }
             // q * d rounded to f16 on packed halves: byte b of a dword becomes
             // the f16 1024 + (b ^ 0x80) (exponent byte 0x64 above it), minus
