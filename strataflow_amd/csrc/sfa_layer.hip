@@ -29,7 +29,11 @@
 
 namespace sfa {
 
-constexpr int kRowsPerWave = 4;
+// expert gate/up rows per wave (one gate and one up row): the waves stay
+// small enough for eight per SIMD and Mixtral's 2 x 14336 rows per slot fill
+// the chip in one pass (79 us for two experts' 470 MB; 2 / 4 / 8 rows per
+// wave: 81 / 89 / 104 us)
+constexpr int kRowsPerWave = 1;
 constexpr int kLayerWaves = 4;
 constexpr int kRowsPerBlock = kRowsPerWave * kLayerWaves;  // expert gate/up rows per workgroup
 
@@ -287,7 +291,7 @@ struct MoeParams {
     const float *weights;    // [n_rows][n_used]
     const void *gate, *up;   // [n_expert][n_ff][n_embd]
     const void *down;        // [n_expert][n_embd][n_ff]
-    float *act;              // [n_rows][n_used][n_ff]
+    float *act;              // [n_rows][n_used][n_ff] (halves for F16 weights)
     float *y;                // [n_rows][n_embd]
     int n_rows, n_embd, n_ff, n_expert, n_used;
 };
@@ -353,7 +357,13 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeParams p) {
         if (lane == r && f0 + r < p.n_ff) {
             // ggml_silu_f32(x) = x / (1 + expf(-x)), times up (swiglu_split)
             const float a = __fmul_rn(__fdiv_rn(gs, __fadd_rn(1.0f, expf(-gs))), us);
-            p.act[((int64_t)t * p.n_used + j) * p.n_ff + f0 + r] = valid ? a : 0.0f;
+            const int64_t ai = ((int64_t)t * p.n_used + j) * p.n_ff + f0 + r;
+            // F16 down weights take the activation rounded to f16 (ggml's
+            // vec_dot_type): stored that way, the down pass loads half the bytes
+            if constexpr (F16)
+                reinterpret_cast<_Float16 *>(p.act)[ai] = valid ? (_Float16)a : (_Float16)0.0f;
+            else
+                p.act[ai] = valid ? a : 0.0f;
         }
     }
 }
@@ -361,8 +371,9 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeParams p) {
 // y[t][o] = (sum over slots j in order of (down[e_j][o] . act[t][j]) * w[t][j])
 // + residual[t][o]; a slot with an id outside [0, n_expert) adds nothing.
 // Every slot's rows stream in the same loop (NU slots, their loads in flight
-// together); two rows per wave, so a 4096-row output has 2048 waves.  Grid
-// (row blocks of n_embd, n_rows).
+// together, four chunks ahead); two rows per wave, so a 4096-row output has
+// 2048 waves.  For F16 weights the activations arrive as halves.  Grid (row
+// blocks of n_embd, n_rows).
 constexpr int kDownRows = 2;
 template <bool F16, int NU>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
@@ -385,12 +396,14 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
         wj[j] = p.weights[(int64_t)t * NU + j];
     }
     const floatx4 *act = reinterpret_cast<const floatx4 *>(p.act + (int64_t)t * NU * p.n_ff);
+    const half8 *act_h = reinterpret_cast<const half8 *>(reinterpret_cast<const _Float16 *>(p.act) +
+                                                         (int64_t)t * NU * p.n_ff);
     float d[NU][kDownRows];
 #pragma unroll
     for (int j = 0; j < NU; ++j)
 #pragma unroll
         for (int r = 0; r < kDownRows; ++r) d[j][r] = 0.0f;
-#pragma unroll 2
+#pragma unroll 4
     for (int c = lane; c < nc; c += 64) {
 #pragma unroll
         for (int j = 0; j < NU; ++j) {
@@ -400,7 +413,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
                 half8 dv[kDownRows];
 #pragma unroll
                 for (int r = 0; r < kDownRows; ++r) dv[r] = D[(mat[j] + rows[r]) * nc + c];
-                const half8 ah = to_half8(ar[2 * c], ar[2 * c + 1]);
+                const half8 ah = act_h[(int64_t)j * nc + c];
 #pragma unroll
                 for (int r = 0; r < kDownRows; ++r) d[j][r] = dot8(dv[r], ah, d[j][r]);
             } else {
