@@ -1297,18 +1297,20 @@ __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeP
     }
 }
 
-// The merge pass of one sequence whose kv-head rows have at most 32 slots
-// (the B = 1 decode up to a few thousand positions): the pass waits on one
-// round of loads, so it is the number of load instructions per wave that sets
-// its length.  Thread t takes dims 4(t % (HD/4)) .. + 3 of the splits
-// t / (HD/4) + NG*i (16-byte loads, NG split groups), every lane the (m, l) of
-// split lane % 32; each group's weighted rows are summed in LDS in group
-// order.  6 loads per thread at HD = 128 instead of 34.
-template <int HD, int G>
+// The merge pass of one sequence whose kv-head rows have at most SM = 32 or
+// 64 slots (the B = 1 decode up to 16k positions, or 32k at 64 splits): the
+// pass waits on one round of loads, so it is the number of load instructions
+// per wave that sets its length.  Thread t takes dims 4(t % (HD/4)) .. + 3 of
+// the splits t / (HD/4) + NG*i (16-byte loads, NG split groups), every lane
+// the (m, l) of split lane % SM; each group's weighted rows are summed in LDS
+// in group order.  At HD = 128, 6 loads per thread for 32 slots and 10 for 64
+// (the general merge issues 34 and 66).
+template <int HD, int G, int SM>
 __global__ __launch_bounds__(256) void decode_merge_small_kernel(DecodeParams p) {
+    static_assert(SM == 32 || SM == 64, "slots");
     constexpr int TPG = HD / 4;             // threads per split group
     constexpr int NG = 256 / TPG;           // split groups
-    constexpr int SPT = (32 + NG - 1) / NG; // splits per thread
+    constexpr int SPT = (SM + NG - 1) / NG; // splits per thread
     __shared__ floatx4 acc_g[NG][TPG];
     const int g = (int)blockIdx.x % G;
     const int kvh = (int)blockIdx.x / G;
@@ -1316,10 +1318,10 @@ __global__ __launch_bounds__(256) void decode_merge_small_kernel(DecodeParams p)
     const int lane = tid & (kWave - 1);
     const int dc = tid % TPG, grp = tid / TPG;
     const int sstride = G * (HD + 4);
-    const int S = p.split_row;  // <= 32
+    const int S = p.split_row;  // <= SM
     const float *row0 = p.part + (int64_t)kvh * S * sstride + g * (HD + 4);
     // every load before seq_len (scalar loads, their own counter) is known
-    const int sl = min(lane & 31, S - 1);
+    const int sl = min(lane & (SM - 1), S - 1);
     const float m_raw = row0[(int64_t)sl * sstride + HD];
     const float l_raw = row0[(int64_t)sl * sstride + HD + 1];
     floatx4 o[SPT];
@@ -1330,7 +1332,7 @@ __global__ __launch_bounds__(256) void decode_merge_small_kernel(DecodeParams p)
     const int n_active = splits_of(sg.n_tiles, p.one_split ? 0 : S - 1, sg.n_tiles);
     if (n_active <= 1) return;  // the split pass wrote the output
 
-    const bool act = (lane & 31) < n_active && lane < 32;
+    const bool act = (lane & (SM - 1)) < n_active && lane < SM;
     const float m = act ? m_raw : -INFINITY;
     const float M = wave_max(m);
     const float w = m != -INFINITY ? __builtin_amdgcn_exp2f(m - M) : 0.0f;  // lane s: split s
@@ -1339,8 +1341,8 @@ __global__ __launch_bounds__(256) void decode_merge_small_kernel(DecodeParams p)
 #pragma unroll
     for (int i = 0; i < SPT; ++i) {
         const int s = grp + NG * i;
-        const float wt = __shfl(w, s & 31, 64);
-        if (s < 32 && wt != 0.0f) {
+        const float wt = __shfl(w, s & (SM - 1), 64);
+        if (s < SM && wt != 0.0f) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[e] = fmaf(o[i][e], wt, acc[e]);
         }
@@ -1424,7 +1426,9 @@ static void launch_merge(const DecodeParams &p, int B, int Hkv, int passes, hipS
         const bool small = p.split_row <= 32;
         if (B == 1) {
             if (small)
-                hipLaunchKernelGGL((decode_merge_small_kernel<HD, G>), dim3(Hkv * G), dim3(256), 0, s, p);
+                hipLaunchKernelGGL((decode_merge_small_kernel<HD, G, 32>), dim3(Hkv * G), dim3(256), 0, s, p);
+            else if (p.split_row <= 64)
+                hipLaunchKernelGGL((decode_merge_small_kernel<HD, G, 64>), dim3(Hkv * G), dim3(256), 0, s, p);
             else
                 hipLaunchKernelGGL((decode_merge_kernel<HD, G, true, 64>), dim3(Hkv * G), dim3(kMergeThreads<HD>),
                                    0, s, p);
