@@ -1198,9 +1198,9 @@ void decode_q8_kernel(DecodeParams p) {
 // A batch sequence without tiles gets a zero output here.  The code is
 // branch-free straight-line work: the pass is latency-bound and each taken
 // branch or instruction-cache miss adds to it.  CH partial rows are loaded
-// per round: 32 when the row has at most 32 slots (one round, no duplicate
-// loads) else 64; the (m, l) of split s sit in lane s % 64 of register s / 64
-// (one register for a row of at most 32 slots).
+// per round (64; 32 would suit a row of at most 32 slots, which the small
+// merges below serve); the (m, l) of split s sit in lane s % 64 of register
+// s / 64.  Rows of at most 64 slots take the small merges.
 template <int HD, int G, bool ONE, int CH>
 __global__ __launch_bounds__(kMergeThreads<HD>) void decode_merge_kernel(DecodeParams p) {
     static_assert(CH == 32 || CH == 64, "round size");
@@ -1361,6 +1361,85 @@ __global__ __launch_bounds__(256) void decode_merge_small_kernel(DecodeParams p)
     }
 }
 
+// The merge pass of a batch whose kv-head rows have at most 64 slots (f16 and
+// F32 batches with 8 or more kv heads): the small single-sequence merge's
+// loads (16-byte loads of split groups, every lane the (m, l) of one split).
+// They go out from the host's guess of the sequence's records (every sequence
+// at max_seq_len: slots b * guess_splits ..) before the plan is known, and
+// again from the planned slots only when the guess was wrong.  A sequence
+// without tiles gets a zero output; one with a single split was written by
+// the split pass.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void decode_merge_batch_small_kernel(DecodeParams p) {
+    constexpr int TPG = HD / 4;             // threads per split group
+    constexpr int NG = 256 / TPG;           // split groups
+    constexpr int SPT = (kWave + NG - 1) / NG;  // splits per thread
+    __shared__ floatx4 acc_g[NG][TPG];
+    const int g = blockIdx.x % G;
+    const int kvh = (blockIdx.x / G) % p.n_head_kv;
+    const int b = blockIdx.x / (G * p.n_head_kv);
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int dc = tid % TPG, grp = tid / TPG;
+    const int sstride = G * (HD + 4);
+    const float *row0 = p.part + (int64_t)kvh * p.split_row * sstride + g * (HD + 4);
+    float m_raw, l_raw;
+    floatx4 o[SPT];
+    // records rec .. rec + S - 1 (indices clamped into them)
+    auto load = [&](int rec, int S) {
+        const float *pg = row0 + (int64_t)rec * sstride;
+        const int sl = min(lane, S - 1);
+        m_raw = pg[(int64_t)sl * sstride + HD];
+        l_raw = pg[(int64_t)sl * sstride + HD + 1];
+#pragma unroll
+        for (int i = 0; i < SPT; ++i)
+            o[i] = *reinterpret_cast<const floatx4 *>(pg + (int64_t)min(grp + NG * i, S - 1) * sstride + 4 * dc);
+    };
+    const int rec_g = b * p.guess_splits;  // the guess stays inside the row
+    load(rec_g, p.guess_splits);
+    const PlanRaw raw = plan_load(p, lane);
+    SlotPlan sp;
+    plan_lanes(p, raw, 0, b, lane, sp);
+    const int n_active = __builtin_amdgcn_readfirstlane(sp.n_b);
+    const int rec0 = __builtin_amdgcn_readfirstlane(sp.rec0);
+    // records past n_active get weight zero, so the guess serves when it
+    // starts at rec0 and covers n_active of them
+    if (n_active > 1 && (rec0 != rec_g || n_active > p.guess_splits)) load(rec0, n_active);
+    float *out = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G + g) * HD;
+    if (n_active <= 1) {
+        if (n_active == 0 && tid < HD) out[tid] = 0.0f;
+        return;
+    }
+
+    const bool act = lane < n_active;
+    const float m = act ? m_raw : -INFINITY;
+    const float M = wave_max(m);
+    const float w = m != -INFINITY ? __builtin_amdgcn_exp2f(m - M) : 0.0f;  // lane s: split s
+    const float L = wave_sum(w != 0.0f ? l_raw * w : 0.0f);
+    floatx4 acc = floatx4{};
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+        const int s = grp + NG * i;
+        const float wt = __shfl(w, s & (kWave - 1), kWave);
+        if (s < kWave && wt != 0.0f) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(o[i][e], wt, acc[e]);
+        }
+    }
+    acc_g[grp][dc] = acc;
+    __syncthreads();
+    if (tid < TPG) {
+        floatx4 O = acc_g[0][tid];
+#pragma unroll
+        for (int k = 1; k < NG; ++k) O += acc_g[k][tid];
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        floatx4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = L > 0.0f ? O[e] * inv : 0.0f;
+        *reinterpret_cast<floatx4 *>(out + 4 * tid) = r;
+    }
+}
+
 // ---- host side -------------------------------------------------------------
 
 struct SplitPlan {
@@ -1433,9 +1512,8 @@ static void launch_merge(const DecodeParams &p, int B, int Hkv, int passes, hipS
                 hipLaunchKernelGGL((decode_merge_kernel<HD, G, true, 64>), dim3(Hkv * G), dim3(kMergeThreads<HD>),
                                    0, s, p);
         } else {
-            if (small)
-                hipLaunchKernelGGL((decode_merge_kernel<HD, G, false, 32>), dim3(B * Hkv * G),
-                                   dim3(kMergeThreads<HD>), 0, s, p);
+            if (p.split_row <= kWave)
+                hipLaunchKernelGGL((decode_merge_batch_small_kernel<HD, G>), dim3(B * Hkv * G), dim3(256), 0, s, p);
             else
                 hipLaunchKernelGGL((decode_merge_kernel<HD, G, false, 64>), dim3(B * Hkv * G),
                                    dim3(kMergeThreads<HD>), 0, s, p);

@@ -57,10 +57,14 @@ def test_decode_wo_vs_float64(gpu, oracle_mod, shape, n_embd, lens, kv_type, wdt
     # against ggml semantics (the oracle's attention)
     ref = _project(c.oracle(oracle_mod.GGML), w, x, wdtype)
     ma, rl = assert_close(y - x, ref - x, what=f"{shape} {wdtype} projection vs ggml")
-    # against the GPU's own two-pass decode output: summation order only
+    # against the GPU's own two-pass decode output: summation order only (the
+    # merge passes add split groups, the fused one splits in order); with f16
+    # weights both round O to f16 first, so a last-ulp order difference can
+    # move one rounding by 2^-11 of that value
     attn = c.decode(max_seq_len=M)
     own = _project(attn, w, x, wdtype)
-    assert_close(y - x, own - x, max_abs=1e-5, rel_l2=1e-5, what="projection vs own decode")
+    assert_close(y - x, own - x, max_abs=1e-5, rel_l2=5e-5 if wdtype == "f16" else 1e-5,
+                 what="projection vs own decode")
     assert np.all(np.isfinite(y))
     # deterministic: a second call gives the same bits
     y2 = c.dev.decode_wo(0, c.t_q, c.t_pt, c.t_sl, M, tw, tx).cpu().numpy()
