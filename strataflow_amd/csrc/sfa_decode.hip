@@ -1361,6 +1361,83 @@ __global__ __launch_bounds__(256) void decode_merge_small_kernel(DecodeParams p)
     }
 }
 
+// The merge pass of one sequence whose kv-head rows have 65 .. 256 slots (B =
+// 1 at long context with few kv heads, or many splits per kv head): one
+// workgroup per (kv head, group head, 32 dims), so the rows' bytes spread over
+// Hkv * g * HD / 32 workgroups and every load goes out in one round.  Thread
+// t takes 4 dims (t % 8) of the splits t / 8 + 32 i; lane s holds the (m, l)
+// of splits s + 64 r; the 32 split groups' weighted sums are added in LDS in
+// group order.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void decode_merge_wide_kernel(DecodeParams p) {
+    constexpr int DQ = HD / 32;                        // 32-dim slices
+    constexpr int RM = kMaxSplits / kWave;             // (m, l) registers per lane
+    constexpr int SPT = kMaxSplits / 32;               // splits per thread
+    static_assert(HD % 32 == 0, "32-dim slices");
+    __shared__ floatx4 acc_g[32][8];
+    const int q4 = (int)blockIdx.x % DQ;
+    const int g = ((int)blockIdx.x / DQ) % G;
+    const int kvh = (int)blockIdx.x / (DQ * G);
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int dc = tid & 7, sg = tid >> 3;
+    const int sstride = G * (HD + 4);
+    const int S = p.split_row;  // <= kMaxSplits
+    const float *row0 = p.part + (int64_t)kvh * S * sstride + g * (HD + 4);
+    // every load before seq_len (scalar loads, their own counter) is known
+    float mv[RM], lv[RM];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        const int sl = min(lane + kWave * r, S - 1);
+        mv[r] = row0[(int64_t)sl * sstride + HD];
+        lv[r] = row0[(int64_t)sl * sstride + HD + 1];
+    }
+    floatx4 o[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; ++i)
+        o[i] = *reinterpret_cast<const floatx4 *>(row0 + (int64_t)min(sg + 32 * i, S - 1) * sstride + 32 * q4 + 4 * dc);
+    const SeqGeom sgeo = seq_geom(p.seq_len[0], p.kv_lo ? p.kv_lo[0] : 0, p.max_pages * p.page_size);
+    const int n_active = splits_of(sgeo.n_tiles, p.one_split ? 0 : S - 1, sgeo.n_tiles);
+    if (n_active <= 1) return;  // the split pass wrote the output
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        mv[r] = lane + kWave * r < n_active ? mv[r] : -INFINITY;
+        mx = fmaxf(mx, mv[r]);
+    }
+    const float M = wave_max(mx);
+    float w[RM], lsum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        w[r] = mv[r] != -INFINITY ? __builtin_amdgcn_exp2f(mv[r] - M) : 0.0f;  // lane s: split s + 64 r
+        lsum += w[r] != 0.0f ? lv[r] * w[r] : 0.0f;
+    }
+    const float L = wave_sum(lsum);
+    floatx4 acc = floatx4{};
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+        // split sg + 32 i sits in lane sg + 32 (i % 2) of register i / 2
+        const float wt = __shfl(w[i / 2], sg + 32 * (i % 2), kWave);
+        if (wt != 0.0f) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(o[i][e], wt, acc[e]);
+        }
+    }
+    acc_g[sg][dc] = acc;
+    __syncthreads();
+    if (tid < 8) {
+        floatx4 O = acc_g[0][tid];
+#pragma unroll
+        for (int k = 1; k < 32; ++k) O += acc_g[k][tid];
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        floatx4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = L > 0.0f ? O[e] * inv : 0.0f;
+        *reinterpret_cast<floatx4 *>(p.out + ((int64_t)kvh * G + g) * HD + 32 * q4 + 4 * tid) = r;
+    }
+}
+
 // The merge pass of a batch whose kv-head rows have at most 64 slots (f16 and
 // F32 batches with 8 or more kv heads): the small single-sequence merge's
 // loads (16-byte loads of split groups, every lane the (m, l) of one split).
@@ -1508,9 +1585,9 @@ static void launch_merge(const DecodeParams &p, int B, int Hkv, int passes, hipS
                 hipLaunchKernelGGL((decode_merge_small_kernel<HD, G, 32>), dim3(Hkv * G), dim3(256), 0, s, p);
             else if (p.split_row <= 64)
                 hipLaunchKernelGGL((decode_merge_small_kernel<HD, G, 64>), dim3(Hkv * G), dim3(256), 0, s, p);
-            else
-                hipLaunchKernelGGL((decode_merge_kernel<HD, G, true, 64>), dim3(Hkv * G), dim3(kMergeThreads<HD>),
-                                   0, s, p);
+            else if constexpr (HD % 32 == 0)
+                hipLaunchKernelGGL((decode_merge_wide_kernel<HD, G>), dim3(Hkv * G * (HD / 32)), dim3(256), 0, s,
+                                   p);
         } else {
             if (p.split_row <= kWave)
                 hipLaunchKernelGGL((decode_merge_batch_small_kernel<HD, G>), dim3(B * Hkv * G), dim3(256), 0, s, p);

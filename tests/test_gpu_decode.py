@@ -326,3 +326,21 @@ def test_decode_f32_batches(gpu, oracle_mod, B):
     out = c.decode(max_seq_len=1600)
     assert_close(out, c.oracle(oracle_mod.GGML), max_abs=F32_MAX_ABS, rel_l2=F32_REL,
                  what=f"f32 B={B}")
+
+
+@pytest.mark.parametrize("kv_type", [0, 1, 8])
+@pytest.mark.parametrize("shape,n_kv", [((16, 2, 128), 20000), ((8, 1, 64), 40000), ((16, 4, 128), 9000),
+                                        ((4, 4, 32), 30000)])
+def test_decode_one_sequence_many_splits(gpu, oracle_mod, kv_type, shape, n_kv):
+    # one sequence whose kv-head rows have 65 .. 256 split records (few kv
+    # heads, long context): the wide merge pass
+    Hq, Hkv, hd = shape
+    if kv_type == 8 and hd < 64:
+        pytest.skip("Q8_0 decode needs head_dim >= 64")
+    c = Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=kv_type,
+             seed=n_kv + Hkv)
+    out = c.decode()
+    if kv_type == 8:
+        assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 {shape} n_kv={n_kv} vs ggml")
+    else:
+        assert_close(out, c.oracle(oracle_mod.GGML), what=f"type {kv_type} {shape} n_kv={n_kv} vs ggml")
