@@ -649,6 +649,125 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     split_merge<HD, G>(lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b);
 }
 
+// One lane's half of a Q8_0 row of K and of V, kept as loaded: head_dim 128,
+// row bytes 68hh .. 68hh + 67 (blocks 2hh and 2hh + 1, 17 dwords); head_dim
+// 64, bytes 32hh .. 32hh + 35 (block hh and two bytes beside it, 9 dwords).
+template <int HD>
+struct Q8Raw {
+    intx4 k4[HD / 32];
+    uint32_t k1;
+    intx4 v4[HD / 32];
+    uint32_t v1;
+};
+
+// The K operand of S = Q8 * K8^T for the lane's row (MFMA column n, quants
+// 16hh .. 16hh + 15 of every block) and the row's block scales, from the two
+// halves' raw pieces.  Half-row dwords D (local byte 0 = row byte 68hh or
+// 32hh).  head_dim 128: the half's first block (2hh) has d at local bytes 0-1
+// and quants 0-15 / 16-31 at 2-17 / 18-33, its second (2hh + 1) d at 34-35
+// and quants at 36-51 / 52-67 (dwords 9-12 / 13-16).  head_dim 64: half 0
+// holds block 0 as the first block above; half 1 (from row byte 32) block 1
+// with d at local 2-3 and quants at dwords 1-4 / 5-8.  Per pair of blocks the
+// lane forms X = its block's quants 0-15 and Y = quants 16-31; swapping X's
+// upper 32 lanes with Y's lower 32 leaves X = the first block of half 0
+// (lanes of half hh holding quants 16hh ..) and Y = that of half 1.
+template <int HD>
+__device__ inline void q8_k_operand(const Q8Raw<HD> &r, int hh, intx4 (&kop)[HD / 32], uint32_t (&kdb)[HD / 32]) {
+    constexpr int KQ = HD / 32, NB = HD / 32;
+    uint32_t D[4 * KQ + 1];
+#pragma unroll
+    for (int j = 0; j < KQ; ++j) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) D[4 * j + e] = (uint32_t)r.k4[j][e];
+    }
+    D[4 * KQ] = r.k1;
+    // bytes 2.. of dwords j, j+1 (head_dim 128, and half 0 of 64); dword
+    // j + 1 itself for half 1 of head_dim 64
+    const uint32_t sel = (HD == 64 && hh) ? 0x07060504u : 0x05040302u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t x = __builtin_amdgcn_perm(D[j + 1], D[j], sel);
+        const uint32_t y = __builtin_amdgcn_perm(D[j + 5], D[j + 4], sel);
+        const auto s = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+        kop[0][j] = (int)s[0];
+        kop[NB / 2][j] = (int)s[1];
+    }
+    if constexpr (HD == 128) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const auto s = __builtin_amdgcn_permlane32_swap(D[9 + j], D[13 + j], false, false);
+            kop[1][j] = (int)s[0];
+            kop[3][j] = (int)s[1];
+        }
+        // d of the half's two blocks (low half of dword 0, high half of dword
+        // 8), then both halves' pairs to every lane
+        const uint32_t dd = __builtin_amdgcn_perm(D[8], D[0], 0x07060100u);
+        const auto s = __builtin_amdgcn_permlane32_swap(dd, dd, false, false);
+        kdb[0] = s[0] & 0xffffu;
+        kdb[1] = s[0] >> 16;
+        kdb[2] = s[1] & 0xffffu;
+        kdb[3] = s[1] >> 16;
+    } else {
+        const uint32_t dd = hh ? D[0] >> 16 : D[0] & 0xffffu;
+        const auto s = __builtin_amdgcn_permlane32_swap(dd, dd, false, false);
+        kdb[0] = s[0];
+        kdb[1] = s[1];
+    }
+}
+
+// The lane's V blocks (VBL = head_dim / 64 of them: blocks VBL*hh ..)
+// dequantised into its row of the f16 LDS tile (`row`, dims 32c .. at byte
+// 64c), or zeros when !keep (a row outside [lo, n_kv): its bytes may be
+// anything).  Block u of the lane's piece spans dwords 8u .. 8u + 8; an even
+// block has d at the low half of its first dword.
+template <int HD>
+__device__ inline void q8_v_row(const Q8Raw<HD> &r, int hh, bool keep, uint8_t *row) {
+    constexpr int KQ = HD / 32, VBL = HD / 64;
+    uint32_t Dv[4 * KQ + 1];
+#pragma unroll
+    for (int j = 0; j < KQ; ++j) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Dv[4 * j + e] = (uint32_t)r.v4[j][e];
+    }
+    Dv[4 * KQ] = r.v1;
+#pragma unroll
+    for (int u = 0; u < VBL; ++u) {
+        const int c = VBL * hh + u;
+        const uint32_t *w = Dv + 8 * u;
+        uint32_t q[8];
+        uint32_t dbits;
+        if ((c & 1) == 0) {
+            dbits = w[0] & 0xffffu;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], 2);
+        } else {
+            dbits = w[0] >> 16;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = w[j + 1];
+        }
+        // q * d rounded to f16 on packed halves: byte b of a dword becomes the
+        // f16 1024 + (b ^ 0x80) (exponent byte 0x64 above it), minus 1152
+        // gives q exactly, and one f16 multiply rounds q * d once, the same
+        // value as rounding the (exact) f32 product.
+        const _Float16 dv = keep ? __builtin_bit_cast(_Float16, (uint16_t)dbits) : (_Float16)0.0f;
+        const half2v dv2 = {dv, dv};
+        const half2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        half8 h[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t x = q[j] ^ 0x80808080u;
+            const half2v lo = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) + bias) * dv2;
+            const half2v hi = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) + bias) * dv2;
+            h[j >> 1][4 * (j & 1) + 0] = lo[0];
+            h[j >> 1][4 * (j & 1) + 1] = lo[1];
+            h[j >> 1][4 * (j & 1) + 2] = hi[0];
+            h[j >> 1][4 * (j & 1) + 3] = hi[1];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) *reinterpret_cast<half8 *>(row + 64 * c + 16 * k) = h[k];
+    }
+}
+
 // Q8_0 decode (head_dim 64 or 128).  A row is head_dim/32 ggml block_q8_0
 // records {fp16 d; int8 q[32]} of 34 bytes; rows start 4-byte aligned (the
 // row is 68 or 136 bytes), so block c starts at 2c mod 4 and every byte
@@ -685,7 +804,6 @@ void decode_q8_kernel(DecodeParams p) {
     constexpr int NB = HD / 32;          // blocks per row
     constexpr int DB = HD / 32;          // 32-dim blocks of the PV output
     constexpr int VROW = HD * 2 + 16;    // padded LDS row of the f16 V tile
-    constexpr int VBL = NB / 2;          // V blocks dequantised per lane
     constexpr int NW = COLS ? kColsWaves : kDecodeWaves;  // most waves per workgroup
     constexpr int QW = COLS ? kColsWaves : 1;             // Q copies (one per kv head)
     constexpr int MW = COLS ? 1 : kDecodeWaves;           // wave records merged in LDS
@@ -731,12 +849,7 @@ void decode_q8_kernel(DecodeParams p) {
     // copied (a copy of a register still being loaded would wait for the
     // load).
     constexpr int KQ = HD / 32;          // 16-byte loads per piece
-    struct Raw {
-        intx4 k4[KQ];
-        uint32_t k1;
-        intx4 v4[KQ];
-        uint32_t v1;
-    };
+    using Raw = Q8Raw<HD>;
     PageWindow pages;
     // Tile t's loads (page id pid, wave-uniform) are buffer loads over the
     // kv head's rows of the tile, issued unconditionally: an invalid page gets
@@ -912,59 +1025,10 @@ void decode_q8_kernel(DecodeParams p) {
         const int pos0 = t * kTile;
         const bool row_ok = pos0 + n >= lo && pos0 + n < n_kv;
         const bool interior = pos0 >= lo && pos0 + kTile <= n_kv;
-        // K operands.  Half-row dwords D (local byte 0 = row byte 68hh or
-        // 32hh).  head_dim 128: the half's first block (2hh) has d at local
-        // bytes 0-1 and quants 0-15 / 16-31 at 2-17 / 18-33, its second
-        // (2hh + 1) d at 34-35 and quants at 36-51 / 52-67 (dwords 9-12 /
-        // 13-16).  head_dim 64: half 0 holds block 0 as the first block
-        // above; half 1 (from row byte 32) block 1 with d at local 2-3 and
-        // quants at dwords 1-4 / 5-8.  Per pair of blocks the lane forms X =
-        // its block's quants 0-15 and Y = quants 16-31; swapping X's upper 32
-        // lanes with Y's lower 32 leaves X = the first block of half 0 (lanes
-        // of half hh holding quants 16hh ..) and Y = that of half 1.
+        // K operands of the row pair (n, both halves)
         intx4 kop[NB];
         uint32_t kdb[NB];
-        {
-            uint32_t D[4 * KQ + 1];
-#pragma unroll
-            for (int j = 0; j < KQ; ++j) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) D[4 * j + e] = (uint32_t)r.k4[j][e];
-            }
-            D[4 * KQ] = r.k1;
-            // bytes 2.. of dwords j, j+1 (head_dim 128, and half 0 of 64);
-            // dword j + 1 itself for half 1 of head_dim 64
-            const uint32_t sel = (HD == 64 && hh) ? 0x07060504u : 0x05040302u;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t x = __builtin_amdgcn_perm(D[j + 1], D[j], sel);
-                const uint32_t y = __builtin_amdgcn_perm(D[j + 5], D[j + 4], sel);
-                const auto s = __builtin_amdgcn_permlane32_swap(x, y, false, false);
-                kop[0][j] = (int)s[0];
-                kop[NB / 2][j] = (int)s[1];
-            }
-            if constexpr (HD == 128) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const auto s = __builtin_amdgcn_permlane32_swap(D[9 + j], D[13 + j], false, false);
-                    kop[1][j] = (int)s[0];
-                    kop[3][j] = (int)s[1];
-                }
-                // d of the half's two blocks (low half of dword 0, high half
-                // of dword 8), then both halves' pairs to every lane
-                const uint32_t dd = __builtin_amdgcn_perm(D[8], D[0], 0x07060100u);
-                const auto s = __builtin_amdgcn_permlane32_swap(dd, dd, false, false);
-                kdb[0] = s[0] & 0xffffu;
-                kdb[1] = s[0] >> 16;
-                kdb[2] = s[1] & 0xffffu;
-                kdb[3] = s[1] >> 16;
-            } else {
-                const uint32_t dd = hh ? D[0] >> 16 : D[0] & 0xffffu;
-                const auto s = __builtin_amdgcn_permlane32_swap(dd, dd, false, false);
-                kdb[0] = s[0];
-                kdb[1] = s[1];
-            }
-        }
+        q8_k_operand<HD>(r, hh, kop, kdb);
         // S = Q8 * K8^T per block, scaled in block order
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = 0.0f;
@@ -978,53 +1042,8 @@ void decode_q8_kernel(DecodeParams p) {
             __builtin_amdgcn_sched_barrier(0);
         }
         // V blocks: dequantise into the f16 LDS tile (rows outside [lo, n_kv)
-        // zeroed).  Block u of the lane's piece spans dwords 8u .. 8u + 8;
-        // an even block has d at the low half of its first dword.
-        uint32_t Dv[4 * KQ + 1];
-#pragma unroll
-        for (int j = 0; j < KQ; ++j) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) Dv[4 * j + e] = (uint32_t)r.v4[j][e];
-        }
-        Dv[4 * KQ] = r.v1;
-#pragma unroll
-        for (int u = 0; u < VBL; ++u) {
-            const int c = VBL * hh + u;
-            const uint32_t *w = Dv + 8 * u;
-            uint32_t q[8];
-            uint32_t dbits;
-            if ((c & 1) == 0) {
-                dbits = w[0] & 0xffffu;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], 2);
-            } else {
-                dbits = w[0] >> 16;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = w[j + 1];
-            }
-            // q * d rounded to f16 on packed halves: byte b of a dword becomes
-            // the f16 1024 + (b ^ 0x80) (exponent byte 0x64 above it), minus
-            // 1152 gives q exactly, and one f16 multiply rounds q * d once,
-            // the same value as rounding the (exact) f32 product.  Rows
-            // outside [lo, n_kv) use d = 0 (their bytes may be anything).
-            const _Float16 dv = (interior || row_ok) ? __builtin_bit_cast(_Float16, (uint16_t)dbits) : (_Float16)0.0f;
-            const half2v dv2 = {dv, dv};
-            const half2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-            half8 h[4];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t x = q[j] ^ 0x80808080u;
-                const half2v lo = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) + bias) * dv2;
-                const half2v hi = (__builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) + bias) * dv2;
-                h[j >> 1][4 * (j & 1) + 0] = lo[0];
-                h[j >> 1][4 * (j & 1) + 1] = lo[1];
-                h[j >> 1][4 * (j & 1) + 2] = hi[0];
-                h[j >> 1][4 * (j & 1) + 3] = hi[1];
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                *reinterpret_cast<half8 *>(vt + n * VROW + 64 * c + 16 * k) = h[k];
-        }
+        // zeroed)
+        q8_v_row<HD>(r, hh, interior || row_ok, vt + n * VROW);
     };
     auto consume2 = [&](int t, float (&sv)[4]) {
         const int pos0 = t * kTile;

@@ -344,3 +344,48 @@ def test_decode_one_sequence_many_splits(gpu, oracle_mod, kv_type, shape, n_kv):
         assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 {shape} n_kv={n_kv} vs ggml")
     else:
         assert_close(out, c.oracle(oracle_mod.GGML), what=f"type {kv_type} {shape} n_kv={n_kv} vs ggml")
+
+
+# ---- Q8_0, one sequence --------------------------------------------------------
+# g = 1..8 and even / odd n_head_kv; short, ragged, windowed and long spans over
+# several page sizes (one split, the 32- and 64-slot merges and the wide merge).
+@pytest.mark.parametrize("shape", [(32, 8, 128), (24, 6, 128), (16, 2, 64), (64, 8, 128), (4, 4, 64),
+                                   (12, 3, 64)])
+@pytest.mark.parametrize("n_kv,lo,page_size", [(1, None, 32), (45, None, 32), (5000, None, 256),
+                                               (3001, 1000, 64), (12345, 17, 32)])
+def test_decode_q8_one_sequence(gpu, oracle_mod, shape, n_kv, lo, page_size):
+    Hq, Hkv, hd = shape
+    c = Case(oracle_mod, seq_lens=[n_kv], kv_lo=None if lo is None else [lo], n_head=Hq, n_head_kv=Hkv,
+             head_dim=hd, page_size=page_size, kv_type=8, seed=n_kv + Hq + hd)
+    out = c.decode()
+    assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 {shape} n_kv={n_kv} lo={lo} vs ggml")
+
+
+def test_decode_q8_one_sequence_placement_and_plans(gpu, oracle_mod):
+    # bit-identical under any physical page order; one split (max_seq_len
+    # small: no merge pass) and a span beyond max_seq_len still match the oracle
+    import torch
+    c = Case(oracle_mod, seq_lens=[5000], kv_lo=[700], kv_type=8, page_size=64, seed=212, extra_pages=5)
+    base = c.decode()
+    assert_close(base, c.oracle(oracle_mod.GGML), what="q8 one sequence window vs ggml")
+    perm = np.random.default_rng(5).permutation(c.n_pages).astype(np.int32)
+    k2 = torch.empty_like(c.dev.k[0]); v2 = torch.empty_like(c.dev.v[0])
+    idx = torch.from_numpy(perm).long().to(gpu)
+    k2[idx] = c.dev.k[0]; v2[idx] = c.dev.v[0]
+    c.dev.k[0].copy_(k2); c.dev.v[0].copy_(v2)
+    pt = c.page_table.copy(); valid = pt >= 0; pt[valid] = perm[pt[valid]]
+    c.t_pt = torch.from_numpy(pt).to(gpu)
+    assert np.array_equal(c.decode().view(np.uint32), base.view(np.uint32))
+    for msl in (100, 1000):
+        assert_close(c.decode(max_seq_len=msl), c.oracle(oracle_mod.GGML), what=f"q8 one sequence msl={msl}")
+
+
+def test_decode_q8_one_sequence_bad_page_id(gpu, oracle_mod):
+    # an out-of-pool page id: the tile's loads get a zero-byte range, it
+    # contributes nothing and the output stays finite
+    import torch
+    c = Case(oracle_mod, seq_lens=[600], page_size=256, kv_type=8, seed=213)
+    pt = c.page_table.copy()
+    pt[0, 1] = c.n_pages + 100
+    c.t_pt = torch.from_numpy(pt).to(gpu)
+    assert np.all(np.isfinite(c.decode()))
