@@ -33,12 +33,14 @@ struct DecodeParams {
     int guess_tiles;      // and of its tiles; the device plan decides
     int one_split;        // 1: no merge pass runs (one sequence, guessed one split)
     int cols_waves;       // Q8_0: kv heads per column-layout workgroup, 0 = per-kv-head layout
+    int staged;           // Q8_0 batches: 1 = decode_q8_staged_kernel (kStagedKv kv heads per wave)
     float scale_log2;     // scale * log2(e)
     float *part;          // [Hkv][split_row][G][HD + 4]: one (o, m, l) record per slot
 };
 
 constexpr int kDecodeWaves = 4;
 constexpr int kColsWaves = 8;    // most waves (kv heads) of a column-layout Q8_0 workgroup
+constexpr int kStagedKv = 4;     // kv heads per wave of the staged Q8_0 kernel
 constexpr int kMaxSplits = 256;  // splits per (sequence, kv head)
 constexpr int kMaxPlanTiles = 1 << 30;  // bound on the tiles of one call (all sequences)
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold: P <= 2^8

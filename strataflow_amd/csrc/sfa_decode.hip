@@ -1206,6 +1206,497 @@ void decode_q8_kernel(DecodeParams p) {
     }
 }
 
+// LDS written by some lanes of a wave and then read by others: a wave's LDS
+// operations complete in order, so only code motion has to be stopped.  (A
+// wavefront-scope fence would also wait for the wave's stage loads into LDS,
+// which are counted with the memory loads.)
+__device__ inline void wave_lds_sync() {
+    __builtin_amdgcn_wave_barrier();
+}
+
+// 32-bit LDS address of a pointer into shared memory
+__device__ inline uint32_t lds_addr32(const uint8_t *ptr) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)(ptr);
+}
+
+// The P^T operand of both PV steps from the lane's row of the wave's P tile
+// (address a = positions 4hh ..): halves 16kk + 0..3 and 16kk + 8..11 into
+// h[2kk] and h[2kk + 1], then the wait for them (asm for the reason below).
+__device__ inline void p_tile_read(uint32_t a, half4 (&h)[4]) {
+    asm volatile(
+        "ds_read_b64 %0, %4\n"
+        "ds_read_b64 %1, %4 offset:16\n"
+        "ds_read_b64 %2, %4 offset:32\n"
+        "ds_read_b64 %3, %4 offset:48\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3])
+        : "v"(a)
+        : "memory");
+}
+
+// The V^T operand reads of one PV step (k block KK) from the f16 V tile at
+// LDS address a: for 32-dim block d and half v, ds_read_b64_tr_b16 at
+// a + (16 KK + 8v) * VROW + 64d into h[2d + v], then the wait for them, in
+// one asm block.  As the builtin, each read would make the compiler wait for
+// every stage load into LDS in flight (it cannot tell the V tile from the
+// stage), which would serialise the next tile's loads with this compute.
+template <int HD, int VROW, int KK>
+__device__ inline void v_tile_tr16(uint32_t a, half4 (&h)[HD / 16]) {
+    constexpr int R0 = 16 * KK * VROW, R1 = (16 * KK + 8) * VROW;
+    if constexpr (HD == 128) {
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %8 offset:%9\n"
+            "ds_read_b64_tr_b16 %1, %8 offset:%10\n"
+            "ds_read_b64_tr_b16 %2, %8 offset:%11\n"
+            "ds_read_b64_tr_b16 %3, %8 offset:%12\n"
+            "ds_read_b64_tr_b16 %4, %8 offset:%13\n"
+            "ds_read_b64_tr_b16 %5, %8 offset:%14\n"
+            "ds_read_b64_tr_b16 %6, %8 offset:%15\n"
+            "ds_read_b64_tr_b16 %7, %8 offset:%16\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3]), "=&v"(h[4]), "=&v"(h[5]), "=&v"(h[6]),
+              "=&v"(h[7])
+            : "v"(a), "n"(R0), "n"(R1), "n"(R0 + 64), "n"(R1 + 64), "n"(R0 + 128), "n"(R1 + 128),
+              "n"(R0 + 192), "n"(R1 + 192)
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %4 offset:%5\n"
+            "ds_read_b64_tr_b16 %1, %4 offset:%6\n"
+            "ds_read_b64_tr_b16 %2, %4 offset:%7\n"
+            "ds_read_b64_tr_b16 %3, %4 offset:%8\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3])
+            : "v"(a), "n"(R0), "n"(R1), "n"(R0 + 64), "n"(R1 + 64)
+            : "memory");
+    }
+}
+
+// Q8_0 decode, batches: R = 4 neighbouring kv heads per wave.  Row n of a
+// 32-row tile is position n / R of the tile's P = 8 positions and kv head
+// kvh0 + n % R of the workgroup's group, so a tile is P runs of R * row_bytes
+// contiguous bytes per tensor.  The wave streams them into its own LDS stage
+// in memory order (global_load_lds, 16 bytes per lane, so every load
+// instruction covers about 1 KB of consecutive bytes), then each lane reads
+// its row piece back from LDS in the layout decode_q8_kernel loads from
+// memory.  Lanes loading row pieces straight from memory touch every cache
+// line of a tile once per load instruction (five per piece), and that cache
+// traffic, not HBM, sets decode_q8_kernel's read rate (3.2 TB/s against about
+// 6 for this loop once it runs).  The kernel's fixed prologue and epilogue are
+// longer, so it serves batches, whose splits give every wave many tiles.
+//   - S = Q8 * K8^T: MFMA rows 8j .. 8j + 7 hold the g heads of kv head j
+//     (row 8j + r is head r % g), so tile row n takes output rows
+//     8(n % R) + 4hh + i, accumulator registers 4(n % R) + i.
+//   - PV: column c of O^T is head c / R of kv head c % R, and the P^T operand
+//     is block diagonal: its row n is zero for the columns of other kv heads
+//     (those entries are cleared once and never written), so one MFMA
+//     sequence per tile serves all R kv heads.
+// The split plan is the per-kv-head layout's (32-position tiles, split_row
+// slots per kv head, the same records), so the merge passes are shared; the
+// 32-position tiles [tile_lo, tile_hi) of a split are R times as many tiles
+// of P positions, which the four waves take in turn.  A tile's stage is read
+// out before the next tile's loads are issued into it, so one tile is in
+// flight while one is computed.
+template <int HD, int G>
+__global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p) {
+    static_assert(HD == 64 || HD == 128, "head_dim");
+    constexpr int R = kStagedKv;
+    static_assert(G >= 1 && G <= 4, "group size");
+    constexpr int NB = HD / 32;        // blocks per row
+    constexpr int DB = HD / 32;        // 32-dim blocks of the PV output
+    constexpr int VROW = HD * 2 + 16;  // padded LDS row of the f16 V tile
+    constexpr int P = kTile / R;       // positions per tile
+    constexpr int C = R * G;           // query heads of the workgroup
+    constexpr int W = kDecodeWaves;
+    constexpr int RB = NB * 34;                       // row bytes
+    constexpr int CR = R * RB / 16;                   // 16-byte chunks per position run
+    constexpr int CT = P * CR;                        // chunks per tensor and tile
+    constexpr int NI = (2 * CT + kWave - 1) / kWave;  // stage load instructions per tile
+    constexpr int PD = HD / 32 * 4 + 1;               // dwords of a lane's row piece
+    static_assert(R * RB % 16 == 0, "runs of whole 16-byte chunks");
+    static_assert(C * HD * 4 <= NI * 1024, "the wave's O^T fits its stage");
+    using Raw = Q8Raw<HD>;
+    typedef __attribute__((address_space(3))) void lds_void;
+
+    // stage: K chunks 0 .. CT-1 then V chunks, 16 bytes each in memory order;
+    // lanes past 2 CT of the last instruction land in its spare tail
+    __shared__ __attribute__((aligned(16))) uint8_t lds_s[W][NI * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[W][kTile * VROW];
+    __shared__ __attribute__((aligned(16))) _Float16 lds_p[W][C][kTile];
+    __shared__ float lds_dq[C][NB];
+    __shared__ intx4 lds_qa[C][NB][2];
+    __shared__ float lds_m[W][C];
+    __shared__ float lds_l[W][C];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 31;  // tile row (QK) / MFMA column (PV)
+    const int hh = lane >> 5;
+    const int kr = n % R;     // kv head of tile row n and of PV column n
+    const int hc = (n / R) % G;  // head of PV column n
+    const int grp = (int)blockIdx.x / p.split_row;
+    const int slot = (int)blockIdx.x - grp * p.split_row;
+    const int kvh0 = grp * R;
+    int b_g = slot / p.guess_splits;  // the host's guess of the slot's sequence / split
+    if (b_g >= p.n_seq) b_g = p.n_seq - 1;
+    const int split_g = slot - b_g * p.guess_splits;
+    const int32_t *pt = p.page_table + (int64_t)b_g * p.max_pages;
+    const int64_t col_bytes = (int64_t)p.n_head_kv * p.row_bytes;
+    uint8_t *vt = lds_v[wave];
+    uint8_t *stage = lds_s[wave];
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+    // Chunk q = 64j + lane of a tile (instruction j): tensor q / CT, position
+    // run (q % CT) / CR, byte 16 ((q % CT) % CR) of the run.  Lanes past the
+    // tile's chunks re-read chunk q - 64 (in bounds; their bytes are unused).
+    int coff[NI];
+    bool cvt[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        int q = kWave * j + lane;
+        if (q >= 2 * CT) q -= kWave;
+        const bool v = q >= CT;
+        const int rq = v ? q - CT : q;
+        coff[j] = (rq / CR) * (int)col_bytes + 16 * (rq % CR);
+        cvt[j] = v;
+    }
+    // Tile u (positions Pu .. Pu + P - 1) of kv heads kvh0 .. kvh0 + R - 1 into
+    // the stage; nothing is issued for an invalid page (false)
+    PageWindow pages;
+    auto issue = [&](int u, int32_t pid) -> bool {
+        const int pos0 = u * P;
+        const int lpage = pos0 / p.page_size;
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        const bool ok = lpage < p.max_pages && kb != nullptr && vb != nullptr;
+        if (ok) {
+            const int64_t off = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh0 * p.row_bytes;
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const uint8_t *src = (cvt[j] ? vb : kb) + off + coff[j];
+                __builtin_amdgcn_global_load_lds(src, (lds_void *)(stage + 1024 * j), 16, 0, 0);
+            }
+        }
+        return ok;
+    };
+    // lane (n, hh)'s row piece from the stage (the bytes the per-kv-head
+    // kernel loads: head_dim 128, row bytes 68hh ..; 64, row bytes 32hh ..)
+    const uint8_t *piece = stage + (n / R) * (R * RB) + kr * RB + (HD == 128 ? 68 : 32) * hh;
+    auto read_stage = [&](Raw &r) {
+        const uint32_t *pk = reinterpret_cast<const uint32_t *>(piece);
+        const uint32_t *pv = reinterpret_cast<const uint32_t *>(piece + CT * 16);
+        uint32_t dk[PD], dv[PD];
+#pragma unroll
+        for (int w = 0; w < PD; ++w) { dk[w] = pk[w]; dv[w] = pv[w]; }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { r.k4[j][e] = (int)dk[4 * j + e]; r.v4[j][e] = (int)dv[4 * j + e]; }
+        }
+        r.k1 = dk[PD - 1];
+        r.v1 = dv[PD - 1];
+    };
+    auto page_of = [&](int u) -> int32_t {
+        const int lpage = u * P / p.page_size;
+        return lpage < p.max_pages ? pages.get(pt, p.max_pages, lpage, lane) : -1;
+    };
+
+    // prologue as in the per-kv-head kernel: page-id window, seq_len / kv_lo
+    // and Q issued before the guessed first tile's K/V burst
+    int t_guess, t_guess_hi;
+    split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
+    const int u_guess = __builtin_amdgcn_readfirstlane(R * t_guess + wave_u);
+    pages.load(pt, p.max_pages, u_guess * P / p.page_size, lane);
+    const PlanRaw raw = plan_load(p, lane);
+    // Q of the C heads kvh0 * g .. of a sequence (one 8-element chunk per
+    // thread)
+    static_assert(C * HD / 8 <= 256, "one Q chunk per thread");
+    const int q_idx = min((int)threadIdx.x, C * HD / 8 - 1);
+    floatx4 qa0, qa1;
+    auto load_q = [&](int bq) {
+        const floatx4 *qr = reinterpret_cast<const floatx4 *>(p.q + ((int64_t)bq * p.n_head + (int64_t)kvh0 * G) * HD);
+        qa0 = qr[2 * q_idx];
+        qa1 = qr[2 * q_idx + 1];
+    };
+    load_q(b_g);
+    bool ok = issue(u_guess, __builtin_amdgcn_readlane(pages.ids, 0));
+
+    SlotPlan sp;
+    if (!plan(p, raw, slot, -1, lane, sp)) {
+        // an idle slot (the merge pass writes the output of a sequence
+        // without tiles); the stage loads land before the workgroup ends
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
+    }
+    const int b = sp.b;
+    int tile_lo, tile_hi;
+    split_tiles(sp.g.t0, sp.g.n_tiles, sp.n_b, sp.split, tile_lo, tile_hi);
+    if (b != b_g) {  // a wrong guess: this slot serves another sequence
+        pt = p.page_table + (int64_t)b * p.max_pages;
+        pages.load(pt, p.max_pages, tile_lo * kTile / p.page_size, lane);
+        load_q(b);
+    }
+    const int u_hi = R * tile_hi;
+    const int lo = sp.g.lo, n_kv = sp.g.n_kv;
+    // Q8_0 of Q (as in the per-kv-head kernel), head hq = chunk / (HD / 8)
+    {
+        const float x[8] = {qa0[0], qa0[1], qa0[2], qa0[3], qa1[0], qa1[1], qa1[2], qa1[3]};
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
+        amax = fmaxf(amax, dpp_row<0xB1>(amax));  // lane ^ 1
+        amax = fmaxf(amax, dpp_row<0x4E>(amax));  // lane ^ 2
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        int w[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int q0 = (int)roundf(x[4 * j] * id), q1 = (int)roundf(x[4 * j + 1] * id);
+            const int q2 = (int)roundf(x[4 * j + 2] * id), q3 = (int)roundf(x[4 * j + 3] * id);
+            w[j] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((int)((unsigned)q3 << 24));
+        }
+        const int idx = threadIdx.x;
+        if (idx < C * HD / 8) {
+            const int hq = idx / (HD / 8), k = idx % (HD / 8);
+            int *dst = reinterpret_cast<int *>(&lds_qa[hq][k >> 2][(k >> 1) & 1]) + 2 * (k & 1);
+            dst[0] = w[0];
+            dst[1] = w[1];
+            if ((k & 3) == 0) lds_dq[hq][k >> 2] = (float)(_Float16)d;
+        }
+    }
+    // the wave's P^T tile starts all zero: entries of another kv head stay so
+    for (int i = lane; i < C * kTile / 8; i += kWave) reinterpret_cast<half8 *>(&lds_p[wave][0][0])[i] = half8{};
+    __syncthreads();
+
+    // A operand row n: head (n % 8) % g of kv head n / 8 (rows past the group
+    // repeat its last kv head; their outputs are not read); d_q of output
+    // rows 8kr + 4hh + i
+    const int hq_a = min(n / 8, R - 1) * G + (n % 8) % G;
+    float dqr[NB][4];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dqr[c][i] = lds_dq[kr * G + (4 * hh + i) % G][c];
+    }
+
+    // the lane's accumulator group (registers 4kr .. 4kr + 3) is picked with
+    // all-ones / zero masks that the optimiser cannot see through: written as
+    // selects between elements of one vector, the choice becomes a
+    // variable-index extract, a compare and select per element
+    int gmask[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        int m = kr == j ? -1 : 0;
+        asm volatile("" : "+v"(m));
+        gmask[j] = m;
+    }
+
+    int u = R * tile_lo + wave_u;
+    if (u != u_guess || b != b_g) {
+        // the guessed tile's loads land before the real ones overwrite the stage
+        __builtin_amdgcn_s_waitcnt(0);
+        ok = u < u_hi ? issue(u, page_of(u)) : false;
+    }
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+    float m_run[G], l_run[G], alpha_h[G];  // of kv head kr
+#pragma unroll
+    for (int h = 0; h < G; ++h) { m_run[h] = -INFINITY; l_run[h] = 0.0f; alpha_h[h] = 1.0f; }
+    bool first = true;
+
+    auto consume1 = [&](int u, const Raw &r, float (&sv)[4]) {
+        const int pos0 = u * P;
+        const bool row_ok = pos0 + n / R >= lo && pos0 + n / R < n_kv;
+        const bool interior = pos0 >= lo && pos0 + P <= n_kv;
+        intx4 kop[NB];
+        uint32_t kdb[NB];
+        q8_k_operand<HD>(r, hh, kop, kdb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lds_qa[hq_a][c][hh], kop[c], intx16{}, 0, 0, 0);
+            const float dk = (float)__builtin_bit_cast(_Float16, (uint16_t)kdb[c]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int a = acc[i] & gmask[0];
+#pragma unroll
+                for (int j = 1; j < R; ++j) a |= acc[4 * j + i] & gmask[j];
+                sv[i] += (float)a * (dk * dqr[c][i]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        q8_v_row<HD>(r, hh, interior || row_ok, vt + n * VROW);
+    };
+    auto consume2 = [&](int u, float (&sv)[4]) {
+        const int pos0 = u * P;
+        const bool row_ok = pos0 + n / R >= lo && pos0 + n / R < n_kv;
+        const bool interior = pos0 >= lo && pos0 + P <= n_kv;
+        // online softmax of kv head kr's heads over the lanes of that kv head
+        // (lanes n' = n mod R, both halves)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = (interior || row_ok) ? sv[i] * p.scale_log2 : -INFINITY;
+        bool exceed = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) exceed |= sv[i] > head_val(m_run, i, hh) + kRescaleLog2;
+        if (__any(exceed)) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float mt = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (head_of<G>(i, hh) == h) mt = fmaxf(mt, sv[i]);
+#pragma unroll
+                for (int off = R; off < 64; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+                const float m_new = fmaxf(m_run[h], mt);
+                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);  // m_run == -inf -> 0
+                l_run[h] *= alpha;
+                alpha_h[h] = alpha;
+                m_run[h] = m_new;
+            }
+            if (!first) {
+                float a = alpha_h[0];
+#pragma unroll
+                for (int h = 1; h < G; ++h) a = hc == h ? alpha_h[h] : a;
+#pragma unroll
+                for (int d = 0; d < DB; ++d) o[d] *= a;
+            }
+        }
+        first = false;
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float mr = head_val(m_run, i, hh);
+            pv[i] = __builtin_amdgcn_exp2f(sv[i] - (mr == -INFINITY ? 0.0f : mr));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (G == 8) {
+                l_run[i] += hh ? 0.0f : pv[i];
+                l_run[4 + i] += hh ? pv[i] : 0.0f;
+            } else if (i < G && hh == 0) {
+                l_run[i] += pv[i];
+            }
+        }
+        // P -> LDS [PV column of (kv head kr, head)][tile row]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i < G || G == 8) lds_p[wave][kr + R * head_of<G>(i, hh)][n] = (_Float16)pv[i];
+        }
+
+        wave_lds_sync();
+
+        half8 pb[2];
+        {
+            half4 a[4];
+            p_tile_read(lds_addr32(reinterpret_cast<const uint8_t *>(&lds_p[wave][kr + R * hc][4 * hh])), a);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { pb[kk][j] = a[2 * kk][j]; pb[kk][4 + j] = a[2 * kk + 1][j]; }
+            }
+        }
+        {
+            const int gq = lane >> 4, rr = lane & 15;
+            const uint8_t *vsrc = vt + (4 * (gq >> 1) + (rr >> 2)) * VROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
+            const uint32_t va_base = lds_addr32(vsrc);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                half4 h[2 * DB];
+                if (kk == 0)
+                    v_tile_tr16<HD, VROW, 0>(va_base, h);
+                else
+                    v_tile_tr16<HD, VROW, 1>(va_base, h);
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+                    half8 va;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { va[e] = h[2 * d][e]; va[4 + e] = h[2 * d + 1][e]; }
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kk], o[d], 0, 0, 0);
+                }
+            }
+        }
+        wave_lds_sync();
+    };
+
+    // per tile: wait for the stage, read it out, issue the next tile into it,
+    // then compute
+    float sv[4];
+    for (; u < u_hi; u += W) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        Raw r;
+        read_stage(r);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int un = u + W;
+        const bool ok_n = un < u_hi ? issue(un, page_of(un)) : false;
+        if (ok) {
+            consume1(u, r, sv);
+            consume2(u, sv);
+        }
+        ok = ok_n;
+    }
+    // no stage load in flight once the loop ends (the last issue was for a
+    // tile past the split): the stages now hold the waves' O^T
+
+    // per-(kv head, head) sums over the lanes of the kv head
+    float Lh[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float v = l_run[h];
+#pragma unroll
+        for (int off = R; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+        Lh[h] = v;
+    }
+    float (*lds_o[W])[HD];
+#pragma unroll
+    for (int w = 0; w < W; ++w) lds_o[w] = reinterpret_cast<float (*)[HD]>(lds_s[w]);
+    float m_col = m_run[0], l_col = Lh[0];
+#pragma unroll
+    for (int h = 1; h < G; ++h)
+        if (hc == h) { m_col = m_run[h]; l_col = Lh[h]; }
+    if (n < C) {
+        if (hh == 0) {
+            lds_m[wave][n] = m_col;
+            lds_l[wave][n] = l_col;
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lds_o[wave][n][32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i];
+        }
+    }
+    __syncthreads();
+    // the waves' (m, l, o) -> the split's record of each (kv head, head), or
+    // the output when the sequence has one split
+    for (int idx = threadIdx.x; idx < C * HD; idx += blockDim.x) {
+        const int c = idx / HD, d = idx % HD;
+        const int kvh = kvh0 + c % R, h = c / R;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, lds_m[w][c]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float mw = lds_m[w][c];
+            const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            L += lds_l[w][c] * wt;
+            O += lds_o[w][c][d] * wt;
+        }
+        if (sp.n_b == 1) {
+            p.out[((int64_t)b * p.n_head + (int64_t)kvh * G + h) * HD + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            float *part = p.part + ((int64_t)kvh * p.split_row + sp.rec0 + sp.split) * G * (HD + 4) + h * (HD + 4);
+            part[d] = O;
+            if (d == 0) {
+                part[HD] = M;
+                part[HD + 1] = L;
+            }
+        }
+    }
+}
+
 // Second pass: out = sum_s o_s * 2^(m_s - M) / sum_s l_s * 2^(m_s - M) over
 // the active splits of each (sequence, kv head), M the largest m_s.  One
 // workgroup per (b, kv head, group head), one thread per dim.  For one
@@ -1580,6 +2071,12 @@ bool use_cols(int kv_type, int HD, int G, int B, int max_seq_len, bool windowed)
     return (long long)B * span_tiles >= kColsMinTiles;
 }
 
+// The staged Q8_0 kernel takes the column layout's batches when its workgroup
+// of kStagedKv kv heads divides the kv heads (g <= 4 already holds there).  It
+// plans the column layout's row: 2048 / Hkv slots, kStagedKv kv heads per
+// four-wave workgroup.
+bool use_staged(int Hkv) { return Hkv % kStagedKv == 0; }
+
 // kv heads per column-layout workgroup: the largest of 8, 4, 2, 1 dividing Hkv
 int cols_waves_of(int Hkv) {
     for (int w = kColsWaves; w > 1; w /= 2)
@@ -1624,6 +2121,11 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
         dim3 grid(p.split_row * Hkv);
         if (p.kv_type == SFA_KV_Q8_0) {
             if constexpr (HD >= 64 && G <= 4) {
+                if (p.staged) {
+                    hipLaunchKernelGGL((decode_q8_staged_kernel<HD, G>), dim3(p.split_row * (Hkv / kStagedKv)),
+                                       dim3(256), 0, s, p);
+                    return launch_merge<HD, G>(p, B, Hkv, passes, s);
+                }
                 if (p.cols_waves > 0) {
                     hipLaunchKernelGGL((decode_q8_kernel<HD, G, true, false>), dim3(p.split_row * (Hkv / p.cols_waves)),
                                        dim3(64 * p.cols_waves), 0, s, p);
@@ -1703,7 +2205,8 @@ int decode_setup(const sfa_kv_desc *kv, const float *q, float *out, const int32_
     p.guess_splits = sp.guess_splits;
     p.guess_tiles = sp.guess_tiles;
     p.one_split = B == 1 && sp.guess_splits == 1;
-    p.cols_waves = cols ? cols_waves_of(Hkv) : 0;
+    p.staged = cols && use_staged(Hkv);
+    p.cols_waves = cols && !p.staged ? cols_waves_of(Hkv) : 0;
     p.scale_log2 = scale * 1.4426950408889634f;
     p.part = static_cast<float *>(workspace);
     p.kv_type = kv->kv_type;
