@@ -240,11 +240,11 @@ def decode_leg(torch, key, lens, kv_type, steps, warmup, seed, cpu_budget_s: flo
     alg = 2 * sum(lens) * HKV * row + len(lens) * HQ * HD * 4 * 2
     us_layer = ms * 1e3 / N_LAYER
     # Q8_0 batches of two or more with >= 1024 tiles in all run the staged
-    # kernel (8 kv heads: two groups of four per slot)
+    # kernel (8 kv heads: whole position columns per workgroup)
     staged = kv_type == 8 and len(lens) >= 2 and len(lens) * ((mx + 31) // 32) >= 1024
     one = "true" if len(lens) == 1 else "false"
     kname = {0: "decode_f32_kernel<128,4>", 1: f"decode_f16_kernel<128,4,{one}>",
-             8: "decode_q8_staged_kernel<128,4>" if staged else f"decode_q8_kernel<128,4,false,{one}>"}[kv_type]
+             8: "decode_q8_staged_kernel<128,4,8>" if staged else f"decode_q8_kernel<128,4,false,{one}>"}[kv_type]
     res = {
         "workload": f"decode-attn {KV_NAMES[kv_type]} KV, Mixtral GQA 32q/8kv hd128, "
                     f"B={len(lens)}, context {lens if len(lens) > 1 else lens[0]}, 256-token pages "

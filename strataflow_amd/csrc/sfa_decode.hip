@@ -1297,31 +1297,32 @@ __device__ inline void v_tile_tr16(uint32_t a, half4 (&h)[HD / 16]) {
 // of P positions, which the four waves take in turn.  A tile's stage is read
 // out before the next tile's loads are issued into it, so one tile is in
 // flight while one is computed.
-template <int HD, int G>
-__global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p) {
+template <int HD, int G, int R>
+__global__ __launch_bounds__(64 * (R == 8 ? 8 : 4), R == 8 ? 1 : 2) void decode_q8_staged_kernel(DecodeParams p) {
     static_assert(HD == 64 || HD == 128, "head_dim");
-    constexpr int R = kStagedKv;
+    static_assert(R == 4 || R == 8, "kv heads per workgroup");
     static_assert(G >= 1 && G <= 4, "group size");
     constexpr int NB = HD / 32;        // blocks per row
     constexpr int DB = HD / 32;        // 32-dim blocks of the PV output
     constexpr int VROW = HD * 2 + 16;  // padded LDS row of the f16 V tile
     constexpr int P = kTile / R;       // positions per tile
     constexpr int C = R * G;           // query heads of the workgroup
-    constexpr int W = kDecodeWaves;
+    constexpr int W = R == 8 ? 8 : 4;  // waves, taking the split's tiles in turn
     constexpr int RB = NB * 34;                       // row bytes
     constexpr int CR = R * RB / 16;                   // 16-byte chunks per position run
     constexpr int CT = P * CR;                        // chunks per tensor and tile
     constexpr int NI = (2 * CT + kWave - 1) / kWave;  // stage load instructions per tile
+    constexpr int SB = 2 * CT * 16;                   // stage bytes (K, then V)
     constexpr int PD = HD / 32 * 4 + 1;               // dwords of a lane's row piece
     static_assert(R * RB % 16 == 0, "runs of whole 16-byte chunks");
-    static_assert(C * HD * 4 <= NI * 1024, "the wave's O^T fits its stage");
+    static_assert(C * HD * 4 <= SB + kTile * VROW, "the wave's O^T fits its stage and V tile");
+    static_assert(C * HD / 8 <= 64 * W, "one Q chunk per thread");
     using Raw = Q8Raw<HD>;
     typedef __attribute__((address_space(3))) void lds_void;
 
-    // stage: K chunks 0 .. CT-1 then V chunks, 16 bytes each in memory order;
-    // lanes past 2 CT of the last instruction land in its spare tail
-    __shared__ __attribute__((aligned(16))) uint8_t lds_s[W][NI * 1024];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_v[W][kTile * VROW];
+    // per wave: the stage (K chunks 0 .. CT-1 then V chunks, 16 bytes each in
+    // memory order), then the f16 V tile; the epilogue reuses both for O^T
+    __shared__ __attribute__((aligned(16))) uint8_t lds_sv[W][SB + kTile * VROW];
     __shared__ __attribute__((aligned(16))) _Float16 lds_p[W][C][kTile];
     __shared__ float lds_dq[C][NB];
     __shared__ intx4 lds_qa[C][NB][2];
@@ -1334,6 +1335,12 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
     const int hh = lane >> 5;
     const int kr = n % R;     // kv head of tile row n and of PV column n
     const int hc = (n / R) % G;  // head of PV column n
+    // R = 4: both lane halves hold the scores of tile row n (MFMA rows
+    // 8kr + 4hh + i are heads (4hh + i) % g of kv head kr).  R = 8: MFMA rows
+    // 4j .. 4j + 3 are kv head j's heads, so output register group jj, half
+    // hh holds kv head 2jj + hh: row n's scores are in half kr % 2 only.
+    const bool valid = R == 4 || hh == (kr & 1);
+    const int jj = R == 4 ? kr : kr >> 1;  // the lane's accumulator register group
     const int grp = (int)blockIdx.x / p.split_row;
     const int slot = (int)blockIdx.x - grp * p.split_row;
     const int kvh0 = grp * R;
@@ -1342,19 +1349,19 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
     const int split_g = slot - b_g * p.guess_splits;
     const int32_t *pt = p.page_table + (int64_t)b_g * p.max_pages;
     const int64_t col_bytes = (int64_t)p.n_head_kv * p.row_bytes;
-    uint8_t *vt = lds_v[wave];
-    uint8_t *stage = lds_s[wave];
+    uint8_t *stage = lds_sv[wave];
+    uint8_t *vt = lds_sv[wave] + SB;
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
     // Chunk q = 64j + lane of a tile (instruction j): tensor q / CT, position
-    // run (q % CT) / CR, byte 16 ((q % CT) % CR) of the run.  Lanes past the
-    // tile's chunks re-read chunk q - 64 (in bounds; their bytes are unused).
+    // run (q % CT) / CR, byte 16 ((q % CT) % CR) of the run.  The last
+    // instruction runs only for the lanes of the tile's last chunks.
     int coff[NI];
     bool cvt[NI];
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
         int q = kWave * j + lane;
-        if (q >= 2 * CT) q -= kWave;
+        if (q >= 2 * CT) q = 2 * CT - 1;
         const bool v = q >= CT;
         const int rq = v ? q - CT : q;
         coff[j] = (rq / CR) * (int)col_bytes + 16 * (rq % CR);
@@ -1374,13 +1381,14 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
                 const uint8_t *src = (cvt[j] ? vb : kb) + off + coff[j];
-                __builtin_amdgcn_global_load_lds(src, (lds_void *)(stage + 1024 * j), 16, 0, 0);
+                if (kWave * j + kWave <= 2 * CT || lane < 2 * CT - kWave * j)
+                    __builtin_amdgcn_global_load_lds(src, (lds_void *)(stage + 1024 * j), 16, 0, 0);
             }
         }
         return ok;
     };
-    // lane (n, hh)'s row piece from the stage (the bytes the per-kv-head
-    // kernel loads: head_dim 128, row bytes 68hh ..; 64, row bytes 32hh ..)
+    // lane (n, hh)'s row piece from the stage (the bytes decode_q8_kernel
+    // loads: head_dim 128, row bytes 68hh ..; 64, row bytes 32hh ..)
     const uint8_t *piece = stage + (n / R) * (R * RB) + kr * RB + (HD == 128 ? 68 : 32) * hh;
     auto read_stage = [&](Raw &r) {
         const uint32_t *pk = reinterpret_cast<const uint32_t *>(piece);
@@ -1401,8 +1409,8 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
         return lpage < p.max_pages ? pages.get(pt, p.max_pages, lpage, lane) : -1;
     };
 
-    // prologue as in the per-kv-head kernel: page-id window, seq_len / kv_lo
-    // and Q issued before the guessed first tile's K/V burst
+    // prologue as in decode_q8_kernel: page-id window, seq_len / kv_lo and Q
+    // issued before the guessed first tile's K/V burst
     int t_guess, t_guess_hi;
     split_tiles(0, p.guess_tiles, p.guess_splits, split_g, t_guess, t_guess_hi);
     const int u_guess = __builtin_amdgcn_readfirstlane(R * t_guess + wave_u);
@@ -1410,7 +1418,6 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
     const PlanRaw raw = plan_load(p, lane);
     // Q of the C heads kvh0 * g .. of a sequence (one 8-element chunk per
     // thread)
-    static_assert(C * HD / 8 <= 256, "one Q chunk per thread");
     const int q_idx = min((int)threadIdx.x, C * HD / 8 - 1);
     floatx4 qa0, qa1;
     auto load_q = [&](int bq) {
@@ -1468,28 +1475,31 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
     for (int i = lane; i < C * kTile / 8; i += kWave) reinterpret_cast<half8 *>(&lds_p[wave][0][0])[i] = half8{};
     __syncthreads();
 
-    // A operand row n: head (n % 8) % g of kv head n / 8 (rows past the group
-    // repeat its last kv head; their outputs are not read); d_q of output
-    // rows 8kr + 4hh + i
-    const int hq_a = min(n / 8, R - 1) * G + (n % 8) % G;
+    // A operand row n: R = 4: head (n % 8) % g of kv head n / 8 (rows past
+    // the group repeat its last kv head; their outputs are not read); R = 8:
+    // head (n % 4) % g of kv head n / 4.  d_q of the lane's output rows.
+    const int hq_a = R == 4 ? min(n / 8, R - 1) * G + (n % 8) % G : (n / 4) * G + (n % 4) % G;
     float dqr[NB][4];
 #pragma unroll
     for (int c = 0; c < NB; ++c) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dqr[c][i] = lds_dq[kr * G + (4 * hh + i) % G][c];
+        for (int i = 0; i < 4; ++i) dqr[c][i] = lds_dq[kr * G + (R == 4 ? (4 * hh + i) : i) % G][c];
     }
 
-    // the lane's accumulator group (registers 4kr .. 4kr + 3) is picked with
+
+    // the lane's accumulator group (registers 4jj .. 4jj + 3) is picked with
     // all-ones / zero masks that the optimiser cannot see through: written as
     // selects between elements of one vector, the choice becomes a
     // variable-index extract, a compare and select per element
-    int gmask[R];
+    int gmask[4];
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
-        int m = kr == j ? -1 : 0;
+    for (int j = 0; j < 4; ++j) {
+        int m = jj == j ? -1 : 0;
         asm volatile("" : "+v"(m));
         gmask[j] = m;
     }
+    // head of the lane's score register i (valid lanes)
+    auto head_i = [&](int i) { return R == 4 ? head_of<G>(i, hh) : i % G; };
 
     int u = R * tile_lo + wave_u;
     if (u != u_guess || b != b_g) {
@@ -1501,7 +1511,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
     floatx16 o[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) o[d] = floatx16{};
-    float m_run[G], l_run[G], alpha_h[G];  // of kv head kr
+    float m_run[G], l_run[G], alpha_h[G];  // of kv head kr (valid lanes)
 #pragma unroll
     for (int h = 0; h < G; ++h) { m_run[h] = -INFINITY; l_run[h] = 0.0f; alpha_h[h] = 1.0f; }
     bool first = true;
@@ -1523,7 +1533,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
             for (int i = 0; i < 4; ++i) {
                 int a = acc[i] & gmask[0];
 #pragma unroll
-                for (int j = 1; j < R; ++j) a |= acc[4 * j + i] & gmask[j];
+                for (int j = 1; j < 4; ++j) a |= acc[4 * j + i] & gmask[j];
                 sv[i] += (float)a * (dk * dqr[c][i]);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -1534,24 +1544,27 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
         const int pos0 = u * P;
         const bool row_ok = pos0 + n / R >= lo && pos0 + n / R < n_kv;
         const bool interior = pos0 >= lo && pos0 + P <= n_kv;
-        // online softmax of kv head kr's heads over the lanes of that kv head
-        // (lanes n' = n mod R, both halves)
+        // online softmax of kv head kr's heads over the lanes holding that kv
+        // head (R = 4: lanes n' = n mod 4, both halves; R = 8: n' = n mod 8 in
+        // half kr % 2)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = (interior || row_ok) ? sv[i] * p.scale_log2 : -INFINITY;
+        for (int i = 0; i < 4; ++i) sv[i] = (valid && (interior || row_ok)) ? sv[i] * p.scale_log2 : -INFINITY;
         bool exceed = false;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) exceed |= sv[i] > head_val(m_run, i, hh) + kRescaleLog2;
+        for (int i = 0; i < 4; ++i) exceed |= sv[i] > m_run[head_i(i)] + kRescaleLog2;
         if (__any(exceed)) {
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 float mt = -INFINITY;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (head_of<G>(i, hh) == h) mt = fmaxf(mt, sv[i]);
+                    if (head_i(i) == h) mt = fmaxf(mt, sv[i]);
 #pragma unroll
-                for (int off = R; off < 64; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+                for (int off = R; off < (R == 4 ? 64 : 32); off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
                 const float m_new = fmaxf(m_run[h], mt);
-                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);  // m_run == -inf -> 0
+                // m_run == -inf -> 0; a lane without this kv head's scores
+                // keeps factor 1
+                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[h] - m_new);
                 l_run[h] *= alpha;
                 alpha_h[h] = alpha;
                 m_run[h] = m_new;
@@ -1560,6 +1573,8 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
                 float a = alpha_h[0];
 #pragma unroll
                 for (int h = 1; h < G; ++h) a = hc == h ? alpha_h[h] : a;
+                // R = 8: PV column n's factor is in the lane holding its scores
+                if constexpr (R == 8) a = valid ? a : xor32(a);
 #pragma unroll
                 for (int d = 0; d < DB; ++d) o[d] *= a;
             }
@@ -1568,22 +1583,19 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
         float pv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float mr = head_val(m_run, i, hh);
+            const float mr = m_run[head_i(i)];
             pv[i] = __builtin_amdgcn_exp2f(sv[i] - (mr == -INFINITY ? 0.0f : mr));
         }
+        // each (kv head, head, position) counted once: R = 4 half 0, R = 8 the
+        // valid half
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (G == 8) {
-                l_run[i] += hh ? 0.0f : pv[i];
-                l_run[4 + i] += hh ? pv[i] : 0.0f;
-            } else if (i < G && hh == 0) {
-                l_run[i] += pv[i];
-            }
+            if (i < G && (R == 8 ? valid : hh == 0)) l_run[i] += pv[i];
         }
         // P -> LDS [PV column of (kv head kr, head)][tile row]
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (i < G || G == 8) lds_p[wave][kr + R * head_of<G>(i, hh)][n] = (_Float16)pv[i];
+            if (i < G && valid) lds_p[wave][kr + R * head_i(i)][n] = (_Float16)pv[i];
         }
 
         wave_lds_sync();
@@ -1638,33 +1650,31 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
         ok = ok_n;
     }
     // no stage load in flight once the loop ends (the last issue was for a
-    // tile past the split): the stages now hold the waves' O^T
+    // tile past the split): stage and V tile now take the waves' O^T
 
-    // per-(kv head, head) sums over the lanes of the kv head
+    // per-(kv head, head) sums over the lanes holding the kv head
     float Lh[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         float v = l_run[h];
 #pragma unroll
-        for (int off = R; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+        for (int off = R; off < (R == 4 ? 64 : 32); off <<= 1) v += __shfl_xor(v, off, 64);
         Lh[h] = v;
     }
-    float (*lds_o[W])[HD];
-#pragma unroll
-    for (int w = 0; w < W; ++w) lds_o[w] = reinterpret_cast<float (*)[HD]>(lds_s[w]);
+    auto lds_o = [&](int w) { return reinterpret_cast<float (*)[HD]>(lds_sv[w]); };
     float m_col = m_run[0], l_col = Lh[0];
 #pragma unroll
     for (int h = 1; h < G; ++h)
         if (hc == h) { m_col = m_run[h]; l_col = Lh[h]; }
     if (n < C) {
-        if (hh == 0) {
+        if (R == 8 ? valid : hh == 0) {
             lds_m[wave][n] = m_col;
             lds_l[wave][n] = l_col;
         }
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) lds_o[wave][n][32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i];
+            for (int i = 0; i < 16; ++i) lds_o(wave)[n][32 * d + 8 * (i >> 2) + 4 * hh + (i & 3)] = o[d][i];
         }
     }
     __syncthreads();
@@ -1682,7 +1692,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_staged_kernel(DecodeParams p
             const float mw = lds_m[w][c];
             const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
             L += lds_l[w][c] * wt;
-            O += lds_o[w][c][d] * wt;
+            O += lds_o(w)[c][d] * wt;
         }
         if (sp.n_b == 1) {
             p.out[((int64_t)b * p.n_head + (int64_t)kvh * G + h) * HD + d] = L > 0.0f ? O / L : 0.0f;
@@ -2122,8 +2132,14 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
         if (p.kv_type == SFA_KV_Q8_0) {
             if constexpr (HD >= 64 && G <= 4) {
                 if (p.staged) {
-                    hipLaunchKernelGGL((decode_q8_staged_kernel<HD, G>), dim3(p.split_row * (Hkv / kStagedKv)),
-                                       dim3(256), 0, s, p);
+                    // eight kv heads (whole position columns) per workgroup
+                    // when 8 | Hkv, else four
+                    if (Hkv % 8 == 0)
+                        hipLaunchKernelGGL((decode_q8_staged_kernel<HD, G, 8>), dim3(p.split_row * (Hkv / 8)),
+                                           dim3(512), 0, s, p);
+                    else
+                        hipLaunchKernelGGL((decode_q8_staged_kernel<HD, G, 4>), dim3(p.split_row * (Hkv / 4)),
+                                           dim3(256), 0, s, p);
                     return launch_merge<HD, G>(p, B, Hkv, passes, s);
                 }
                 if (p.cols_waves > 0) {
