@@ -239,10 +239,12 @@ def test_decode_split_plan_batches(gpu, oracle_mod, kv_type, B):
     assert np.all(out[0] == 0)
 
 
-@pytest.mark.parametrize("shape", [(8, 8, 128), (8, 4, 64), (12, 6, 64), (4, 1, 128)])
+@pytest.mark.parametrize("shape", [(8, 8, 128), (8, 4, 64), (12, 6, 64), (4, 1, 128), (64, 16, 128),
+                                   (48, 12, 64), (16, 8, 64)])
 def test_decode_q8_column_layout(gpu, oracle_mod, shape):
-    # a batch with >= 1024 tiles in all takes the Q8_0 column layout (one wave
-    # per kv head, workgroups of 8, 4, 2 or 1 kv heads for these shapes)
+    # a batch with >= 1024 tiles in all takes the staged kernel when 4 | Hkv
+    # (8 kv heads per workgroup when 8 | Hkv: Hkv 8, 16; else 4: Hkv 4, 12),
+    # otherwise the column layout (one wave per kv head: Hkv 6, 1)
     Hq, Hkv, hd = shape
     B = 40
     rng = np.random.default_rng(300 + Hkv)
@@ -387,5 +389,40 @@ def test_decode_q8_one_sequence_bad_page_id(gpu, oracle_mod):
     c = Case(oracle_mod, seq_lens=[600], page_size=256, kv_type=8, seed=213)
     pt = c.page_table.copy()
     pt[0, 1] = c.n_pages + 100
+    c.t_pt = torch.from_numpy(pt).to(gpu)
+    assert np.all(np.isfinite(c.decode()))
+
+
+# ---- Q8_0 batches on the staged kernel: windows, page sizes, placement ----------
+@pytest.mark.parametrize("Hkv,page_size", [(8, 32), (8, 256), (4, 64)])
+def test_decode_q8_staged_windows(gpu, oracle_mod, Hkv, page_size):
+    # 4 sequences of 3000..9000 positions (>= 1024 tiles in all), window
+    # starts on and off the 32-position grid, one empty sequence
+    lens = [9000, 3001, 0, 7777]
+    lo = [4000, 17, 0, 3]
+    c = Case(oracle_mod, seq_lens=lens, kv_lo=lo, n_head=4 * Hkv, n_head_kv=Hkv, head_dim=128,
+             page_size=page_size, kv_type=8, seed=320 + Hkv + page_size)
+    out = c.decode(max_seq_len=9000)
+    assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 staged window Hkv={Hkv} page={page_size} vs ggml")
+    assert np.all(out[2] == 0)
+
+
+def test_decode_q8_staged_placement_and_bad_page(gpu, oracle_mod):
+    # bit-identical under any physical page order; an out-of-pool page id in
+    # one sequence leaves every output finite
+    import torch
+    lens = [9000, 8000, 6000, 3000]  # 4 x 282 tiles: the staged kernel
+    c = Case(oracle_mod, seq_lens=lens, kv_type=8, page_size=64, seed=330, extra_pages=5)
+    base = c.decode()
+    assert_close(base, c.oracle(oracle_mod.GGML), what="q8 staged batch vs ggml")
+    perm = np.random.default_rng(7).permutation(c.n_pages).astype(np.int32)
+    k2 = torch.empty_like(c.dev.k[0]); v2 = torch.empty_like(c.dev.v[0])
+    idx = torch.from_numpy(perm).long().to(gpu)
+    k2[idx] = c.dev.k[0]; v2[idx] = c.dev.v[0]
+    c.dev.k[0].copy_(k2); c.dev.v[0].copy_(v2)
+    pt = c.page_table.copy(); valid = pt >= 0; pt[valid] = perm[pt[valid]]
+    c.t_pt = torch.from_numpy(pt).to(gpu)
+    assert np.array_equal(c.decode().view(np.uint32), base.view(np.uint32))
+    pt[1, 3] = c.n_pages + 100
     c.t_pt = torch.from_numpy(pt).to(gpu)
     assert np.all(np.isfinite(c.decode()))
