@@ -91,6 +91,20 @@ def test_desc_check_rejects(field, value, status):
     assert lib.sfa_kv_desc_check(ctypes.byref(desc(**{field: value}))) == status
 
 
+def test_q8_0_head_dim_32_is_unsupported_for_attention():
+    """A Q8_0 cache with head_dim 32 is appended to (the RoPE + append kernel
+    takes it) but not attended over: decode and prefill return
+    SFA_ERR_UNSUPPORTED from their host checks, before any device work."""
+    lib = _lib.load()
+    d = desc(kv_type=_lib.SFA_KV_Q8_0, head_dim=32)
+    assert lib.sfa_kv_desc_check(ctypes.byref(d)) == _lib.SFA_OK
+    p = 0x1000  # never dereferenced
+    ws = lib.sfa_decode_workspace_bytes(ctypes.byref(d), 1, 256)
+    assert lib.sfa_attn_decode(ctypes.byref(d), p, p, p, 4, p, None, 1, 256, 0.1, p, ws,
+                               None) == _lib.SFA_ERR_UNSUPPORTED
+    assert lib.sfa_attn_prefill(ctypes.byref(d), p, p, p, 4, 0, 16, 0, 0.1, None) == _lib.SFA_ERR_UNSUPPORTED
+
+
 def test_page_table_check():
     import numpy as np
     lib = _lib.load()
