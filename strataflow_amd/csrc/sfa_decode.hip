@@ -1573,8 +1573,17 @@ __global__ __launch_bounds__(64 * (R == 8 ? 8 : 4), R == 8 ? 1 : 2) void decode_
                 float a = alpha_h[0];
 #pragma unroll
                 for (int h = 1; h < G; ++h) a = hc == h ? alpha_h[h] : a;
-                // R = 8: PV column n's factor is in the lane holding its scores
-                if constexpr (R == 8) a = valid ? a : xor32(a);
+                // R = 8: PV column n's factor is in the lane holding its scores.
+                // Every lane takes part in the exchange: written as
+                // valid ? a : xor32(a), the compiler ran the lane exchange
+                // only in the lanes that use it, with their partner lanes
+                // switched off, so it read nothing from them.  The empty asm
+                // keeps the exchange in the uniform code.
+                if constexpr (R == 8) {
+                    float ax = xor32(a);
+                    asm volatile("" : "+v"(ax));
+                    a = valid ? a : ax;
+                }
 #pragma unroll
                 for (int d = 0; d < DB; ++d) o[d] *= a;
             }

@@ -68,7 +68,7 @@ class Case:
 
     def __init__(self, oracle_mod, *, seq_lens, n_head=32, n_head_kv=8, head_dim=128,
                  page_size=256, kv_type=1, seed=0, extra_pages=3, kv_lo=None, freq_base=1e6,
-                 n_layer=1, device="cuda"):
+                 n_layer=1, device="cuda", k_boost=None):
         import torch
 
         from strataflow_amd import synth
@@ -90,6 +90,11 @@ class Case:
                 continue
             pos = np.arange(n, dtype=np.int32)
             _, k, v = synth.qkv(rng, n, 1, n_head_kv, head_dim, pos, freq_base)
+            if k_boost is not None:
+                # (period, phase, factor): keys at positions p % period ==
+                # phase scaled, so later tiles hold scores far above earlier ones
+                period, phase, factor = k_boost
+                k[pos % period == phase] *= factor
             assert self.host.append(k, v, np.full(n, b, np.int32), pos, self.page_table) == 0
         qpos = np.maximum(self.seq_lens - 1, 0)
         self.q = np.stack([synth.qkv(rng, 1, n_head, n_head_kv, head_dim, np.array([p]), freq_base)[0][0]
