@@ -423,6 +423,23 @@ def test_decode_q8_staged_late_rescale(gpu, oracle_mod, n_head_kv):
     out = c.decode()
     assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 staged Hkv={n_head_kv} late rescale vs ggml")
 
+@pytest.mark.parametrize("kv_type", [0, 1, 8])
+@pytest.mark.parametrize("lens,shape", [([20000], (32, 8, 128)), ([12000, 5000, 9000], (16, 2, 128)),
+                                        ([3000, 7000], (8, 8, 64))])
+def test_decode_late_rescale(gpu, oracle_mod, kv_type, lens, shape):
+    # every 61st key scaled x5, so waves whose first tile misses those keys
+    # rescale O and l mid-split: one sequence, a batch (the Q8_0 column layout
+    # for two kv heads) and head_dim 64
+    Hq, Hkv, hd = shape
+    c = Case(oracle_mod, seq_lens=lens, n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=kv_type,
+             seed=600 + kv_type + len(lens), k_boost=(61, 30, 5.0))
+    out = c.decode()
+    what = f"type {kv_type} {shape} B={len(lens)} late rescale vs ggml"
+    if kv_type == 0:
+        assert_close(out, c.oracle(oracle_mod.GGML), max_abs=F32_MAX_ABS, rel_l2=F32_REL, what=what)
+    else:
+        assert_close(out, c.oracle(oracle_mod.GGML), what=what)
+
 def test_decode_q8_staged_placement_and_bad_page(gpu, oracle_mod):
     # bit-identical under any physical page order; an out-of-pool page id in
     # one sequence leaves every output finite

@@ -10,7 +10,8 @@ from tests.helpers import assert_close, f16_cols, golden, scatter_columns
 pytestmark = pytest.mark.gpu
 
 
-def build(oracle_mod, gpu, *, Hq, Hkv, hd, n_cached, T, page_size=256, seed=0, bf16=False, kv_type=1):
+def build(oracle_mod, gpu, *, Hq, Hkv, hd, n_cached, T, page_size=256, seed=0, bf16=False, kv_type=1,
+          k_boost=None):
     import torch
     from strataflow_amd import synth
     from strataflow_amd.paged_kv import PagedKV
@@ -21,6 +22,10 @@ def build(oracle_mod, gpu, *, Hq, Hkv, hd, n_cached, T, page_size=256, seed=0, b
     host = oracle_mod.HostPagedKv(Hkv, hd, page_size, kv_type, n_pages)
     pos = np.arange(n_kv, dtype=np.int32)
     q, k, v = synth.qkv(rng, n_kv, Hq, Hkv, hd, pos, 1e6, bf16=bf16)
+    if k_boost is not None:
+        # (period, phase, factor): keys at positions p % period == phase scaled
+        period, phase, factor = k_boost
+        k[pos % period == phase] *= factor
     assert host.append(k, v, np.zeros(n_kv, np.int32), pos, pt) == 0
     q = np.ascontiguousarray(q[n_cached:])
     dev = PagedKV(1, Hq, Hkv, hd, kv_type, page_size, n_pages, device=gpu)
@@ -232,3 +237,20 @@ def test_prefill_q8_rows_match_q8_decode(gpu, oracle_mod):
     sl = torch.tensor([n_cached + t + 1 for t in rows], dtype=torch.int32, device=gpu)
     dec = dev.decode(0, tq, tpt, sl, n_kv).cpu().numpy().reshape(len(rows), -1)
     assert_close(out[rows], dec, max_abs=1e-3, rel_l2=5e-4, what="q8 prefill rows vs decode")
+
+
+@pytest.mark.parametrize("kv_type", [0, 1, 8])
+def test_prefill_late_rescale(gpu, oracle_mod, kv_type):
+    # every 200th key from position 150 scaled x5: each row's first 64-position
+    # tile holds ordinary scores and a later tile scores far above them, so the
+    # lazy reference moves and O and l are rescaled after the first tile
+    Hq, Hkv, hd, n_cached, T = 32, 8, 128, 1500, 256
+    host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=Hq, Hkv=Hkv, hd=hd, n_cached=n_cached, T=T,
+                                   seed=500 + kv_type, kv_type=kv_type, k_boost=(200, 150, 5.0))
+    out = run(dev, gpu, pt, q, n_cached)
+    ref = host.attention(q[None], Hq, pt, np.array([n_kv], np.int32), None,
+                         T=T, mode=oracle_mod.GGML)[0].reshape(T, -1)
+    if kv_type == 0:
+        assert_close(out, ref, max_abs=F32_MAX_ABS, rel_l2=F32_REL, what="f32 late rescale vs ggml")
+    else:
+        assert_close(out, ref, what=f"type {kv_type} late rescale vs ggml")
