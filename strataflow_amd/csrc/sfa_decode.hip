@@ -1687,22 +1687,34 @@ __global__ __launch_bounds__(64 * (R == 8 ? 8 : 4), R == 8 ? 1 : 2) void decode_
         }
     }
     __syncthreads();
-    // the waves' (m, l, o) -> the split's record of each (kv head, head), or
-    // the output when the sequence has one split
-    for (int idx = threadIdx.x; idx < C * HD; idx += blockDim.x) {
-        const int c = idx / HD, d = idx % HD;
-        const int kvh = kvh0 + c % R, h = c / R;
+    // each column's wave weights once, one thread per column, in place:
+    // lds_m[w][c] <- wave w's weight 2^(m_w - M), lds_l[0][c] <- L, lds_l[1][c] <- M
+    if ((int)threadIdx.x < C) {
+        const int c = threadIdx.x;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < W; ++w) M = fmaxf(M, lds_m[w][c]);
-        float L = 0.0f, O = 0.0f;
+        float L = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             const float mw = lds_m[w][c];
             const float wt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
             L += lds_l[w][c] * wt;
-            O += lds_o(w)[c][d] * wt;
+            lds_m[w][c] = wt;
         }
+        lds_l[0][c] = L;
+        lds_l[1][c] = M;
+    }
+    __syncthreads();
+    // the waves' (m, l, o) -> the split's record of each (kv head, head), or
+    // the output when the sequence has one split
+    for (int idx = threadIdx.x; idx < C * HD; idx += blockDim.x) {
+        const int c = idx / HD, d = idx % HD;
+        const int kvh = kvh0 + c % R, h = c / R;
+        float O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) O += lds_o(w)[c][d] * lds_m[w][c];
+        const float L = lds_l[0][c], M = lds_l[1][c];
         if (sp.n_b == 1) {
             p.out[((int64_t)b * p.n_head + (int64_t)kvh * G + h) * HD + d] = L > 0.0f ? O / L : 0.0f;
         } else {
