@@ -1328,8 +1328,6 @@ __global__ __launch_bounds__(64 * (R == 8 ? 8 : 4), R == 8 ? 1 : 2) void decode_
     __shared__ intx4 lds_qa[C][NB][2];
     __shared__ float lds_m[W][C];
     __shared__ float lds_l[W][C];
-    // sink of the L2 prefetch loads below; never read
-    __shared__ __attribute__((aligned(16))) uint8_t lds_pf[256];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -1409,36 +1407,6 @@ __global__ __launch_bounds__(64 * (R == 8 ? 8 : 4), R == 8 ? 1 : 2) void decode_
     auto page_of = [&](int u) -> int32_t {
         const int lpage = u * P / p.page_size;
         return lpage < p.max_pages ? pages.get(pt, p.max_pages, lpage, lane) : -1;
-    };
-    // L2 prefetch of a later tile: one dword of every 64-byte line of its K
-    // and V runs, loaded into a sink the kernel never reads, so the tile's own
-    // stage loads, issued a tile later, find its lines in L2.  Lane slot
-    // 64j + lane covers line q of the tile's K runs, then of its V runs.
-    constexpr int LPT = CT * 16 / 64;  // 64-byte lines per tensor and tile
-    constexpr int NPF = (2 * LPT + kWave - 1) / kWave;
-    int pf_off[NPF];
-    bool pf_v[NPF];
-#pragma unroll
-    for (int j = 0; j < NPF; ++j) {
-        const int q = min(kWave * j + lane, 2 * LPT - 1);
-        pf_v[j] = q >= LPT;
-        const int byte = 64 * (pf_v[j] ? q - LPT : q);
-        pf_off[j] = (byte / (R * RB)) * (int)col_bytes + byte % (R * RB);
-    }
-    auto prefetch = [&](int u) {
-        const int pos0 = u * P;
-        const int lpage = pos0 / p.page_size;
-        const int32_t pid = page_of(u);
-        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
-        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
-        if (lpage < p.max_pages && kb != nullptr && vb != nullptr) {
-            const int64_t off = (int64_t)(pos0 - lpage * p.page_size) * col_bytes + (int64_t)kvh0 * p.row_bytes;
-#pragma unroll
-            for (int j = 0; j < NPF; ++j) {
-                if (kWave * j + kWave <= 2 * LPT || lane < 2 * LPT - kWave * j)
-                    __builtin_amdgcn_global_load_lds((pf_v[j] ? vb : kb) + off + pf_off[j], (lds_void *)lds_pf, 4, 0, 0);
-            }
-        }
     };
 
     // prologue as in decode_q8_kernel: page-id window, seq_len / kv_lo and Q
@@ -1684,16 +1652,14 @@ __global__ __launch_bounds__(64 * (R == 8 ? 8 : 4), R == 8 ? 1 : 2) void decode_
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int un = u + W;
         const bool ok_n = un < u_hi ? issue(un, page_of(un)) : false;
-        if (un + W < u_hi) prefetch(un + W);
         if (ok) {
             consume1(u, r, sv);
             consume2(u, sv);
         }
         ok = ok_n;
     }
-    // nothing in flight past this wait (the last stage issue and prefetch
-    // were for tiles past the split): stage and V tile now take the waves' O^T
-    __builtin_amdgcn_s_waitcnt(0);
+    // no stage load in flight once the loop ends (the last issue was for a
+    // tile past the split): stage and V tile now take the waves' O^T
 
     // per-(kv head, head) sums over the lanes holding the kv head
     float Lh[G];
