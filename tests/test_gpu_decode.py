@@ -412,16 +412,18 @@ def test_decode_q8_staged_windows(gpu, oracle_mod, Hkv, page_size):
     assert np.all(out[2] == 0)
 
 
+@pytest.mark.parametrize("head_dim", [128, 64])
 @pytest.mark.parametrize("n_head_kv", [8, 4])
-def test_decode_q8_staged_late_rescale(gpu, oracle_mod, n_head_kv):
+def test_decode_q8_staged_late_rescale(gpu, oracle_mod, n_head_kv, head_dim):
     # every 61st key scaled x5: most waves of the staged kernel (eight and
     # four kv heads per workgroup) meet scores more than the lazy-rescale
     # margin above their running reference after their first tile, so O and
     # l are rescaled mid-split in both halves of the lanes
     c = Case(oracle_mod, seq_lens=[12000, 5000, 9000], n_head=4 * n_head_kv, n_head_kv=n_head_kv,
-             head_dim=128, kv_type=8, seed=400 + n_head_kv, k_boost=(61, 30, 5.0))
+             head_dim=head_dim, kv_type=8, seed=400 + n_head_kv + head_dim, k_boost=(61, 30, 5.0))
     out = c.decode()
-    assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 staged Hkv={n_head_kv} late rescale vs ggml")
+    assert_close(out, c.oracle(oracle_mod.GGML),
+                 what=f"q8 staged Hkv={n_head_kv} hd={head_dim} late rescale vs ggml")
 
 @pytest.mark.parametrize("kv_type", [0, 1, 8])
 @pytest.mark.parametrize("lens,shape", [([20000], (32, 8, 128)), ([12000, 5000, 9000], (16, 2, 128)),
