@@ -179,9 +179,21 @@ def hbm_roofline(alg_bytes: int, k_mean_us: float, node_us: float, kernel: str, 
         "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
         "kernel_us_mean": round(k_mean_us, 3), "bytes_per_launch": alg_bytes,
-        "node": {"us": round(node_us, 3), "achieved": round(node, 1), "frac": round(node / HBM_PEAK_GBS, 4),
-                 "what": "the whole attention node per layer (split pass, merge pass, launch gaps) "
-                         "from the graph-replayed step"}}, key)
+        # the whole attention node per layer (split pass, merge pass, launch
+        # gaps) from the graph-replayed step
+        "node_us": round(node_us, 3), "node_achieved": round(node, 1),
+        "node_frac": round(node / HBM_PEAK_GBS, 4)}, key)
+
+
+def flat(prefix: str, d: dict) -> dict:
+    """d's fields under prefix + name, nested objects flattened the same way."""
+    out = {}
+    for k, v in d.items():
+        if isinstance(v, dict):
+            out.update(flat(f"{prefix}{k}_", v))
+        else:
+            out[prefix + k] = v
+    return out
 
 
 def load_traffic() -> dict:
@@ -203,14 +215,18 @@ def with_traffic(roofline: dict, key: str) -> dict:
     around back-to-back launches)."""
     t = load_traffic().get(key)
     if t:
-        roofline["traffic"] = t["bytes_per_launch"]
+        roofline["traffic"] = t.get("bytes_per_launch")
         roofline["traffic_source"] = f"profiles/traffic.json[{key}] (rocprofv3 FETCH_SIZE+WRITE_SIZE)"
         work = roofline.get("bytes_per_launch") or roofline.get("flop_per_launch")
         if work and t.get("kernel_us_mean"):
             ach = work / (t["kernel_us_mean"] * 1e-6) / (1e9 if roofline["unit"] == "GB/s" else 1e12)
-            roofline["rocprof"] = {"kernel_us_mean": t["kernel_us_mean"], "achieved": round(ach, 1),
-                                   "frac": round(ach / roofline["peak"], 4),
-                                   "source": t.get("profile") or "profiles/"}
+            roofline["rocprof_kernel_us_mean"] = t["kernel_us_mean"]
+            roofline["rocprof_achieved"] = round(ach, 1)
+            roofline["rocprof_frac"] = round(ach / roofline["peak"], 4)
+            roofline["rocprof_source"] = t.get("profile") or "profiles/"
+        for k in ("mfma_busy", "valu_busy", "lds_bank_conflict_frac"):
+            if t.get(k) is not None:
+                roofline[f"rocprof_{k}"] = t[k]
     return roofline
 
 
@@ -368,23 +384,25 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1, c
                       sample_1t="kv head 0 of layer 0 (its 4 query heads, the whole chunk), times 8 "
                                 "kv heads; ggml-semantics oracle with the causal mask",
                       gpu_out=out0)
+    # one flat object (roofline and CPU baseline fields side by side) so that
+    # every figure survives a reader that keeps scalar fields only
     res = {
         "workload": f"causal prefill {name} KV, 2048-token chunk on 2048 cached, Mixtral GQA 32q/8kv hd128",
         "us_per_layer_chunk": round(us, 2),
         "us_per_layer_token": round(us / T, 5),
         "tflops": round(tflops, 1),
-        "roofline": with_traffic({"bound": "mfma", "achieved": round(tflops, 1),
-                                  "peak": peak, "unit": "TFLOP/s",
-                                  "frac": round(tflops / peak, 4), "traffic": None,
-                                  "kernel": {0: "prefill_f32_kernel<128,4>", 1: "prefill_f16_kernel<128,4>",
-                                             8: "prefill_q8_kernel<128,4>"}[kv_type],
-                                  "flop_per_launch": flops},
-                                 {1: "prefill_2048_on_2048", 0: "prefill_f32_2048_on_2048",
-                                  8: "prefill_q8_0_2048_on_2048"}[kv_type]),
         "flop_per_layer_chunk": flops,
     }
+    res.update(with_traffic({"bound": "mfma", "achieved": round(tflops, 1),
+                             "peak": peak, "unit": "TFLOP/s",
+                             "frac": round(tflops / peak, 4), "traffic": None,
+                             "kernel": {0: "prefill_f32_kernel<128,4>", 1: "prefill_f16_kernel<128,4>",
+                                        8: "prefill_q8_kernel<128,4>"}[kv_type],
+                             "flop_per_launch": flops},
+                            {1: "prefill_2048_on_2048", 0: "prefill_f32_2048_on_2048",
+                             8: "prefill_q8_0_2048_on_2048"}[kv_type]))
     if cpu is not None:
-        res["cpu_baseline"] = cpu
+        res.update(flat("cpu_", cpu))
     del kv, qs, out
     torch.cuda.empty_cache()
     return res
@@ -622,14 +640,19 @@ def window_cpu_leg(B: int, hist: int, W: int, lossless: bool, budget_s: float, s
                    "us/layer-step", 1e6, what + ", ggml-semantics oracle, seeded f16 values", budget_s)
 
 
-def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 8, cpu_budget_s: float = 0.0):
+def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 128, cpu_budget_s: float = 0.0,
+                 lossless_layers: int = 4):
     """KV-window decode under paging pressure: 4 sequences with 65536-token
     histories, a 4096-position window, the device pool sized to the window
     (4 x 17 pages per layer), pages evicted and reused by the host page
-    manager every 256 steps of a sequence, all 32 layers.  (a) the opt-in
-    sliding window for `steps` decode steps; (b) the reference's lossless
+    manager every 256 steps of a sequence.  (a) the opt-in sliding window for
+    `steps` decode steps over all 32 layers; (b) the reference's lossless
     semantics (every position attended, the evicted positions read from the
-    host-pinned cold pool in place) for `lossless_steps` steps."""
+    host-pinned cold pool in place) for `lossless_steps` steps over
+    `lossless_layers` layers: a lossless layer-step reads 1 GB of cold pages
+    over the host link (about 20 ms), so 128 steps of 32 layers would hold
+    the GPU for 80 s; the per-layer-step cost does not depend on the layer
+    count."""
     from strataflow_amd import _lib, synth
     from strataflow_amd.pager import SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, KvPager
     dev = torch.device("cuda:0")
@@ -638,7 +661,7 @@ def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 8, cp
     res = {}
     for name, attend, n_steps in (("sliding_window", SFA_ATTEND_WINDOW, steps),
                                   ("lossless", SFA_ATTEND_LOSSLESS, lossless_steps)):
-        n_layer = N_LAYER
+        n_layer = N_LAYER if attend == SFA_ATTEND_WINDOW else lossless_layers
         pager = KvPager(n_layer=n_layer, n_head=HQ, n_head_kv=HKV, head_dim=HD, kv_type=SFA_KV_F16,
                         page_size=PAGE, n_seq=B, n_ctx=hist + n_steps, window=W, attend=attend,
                         seed=seed)
@@ -754,8 +777,8 @@ def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 8, cp
                 "unit": "GB/s", "frac": round(ach / HOST_LINK_PEAK_GBS, 4), "traffic": None,
                 "kernel": kname, "kernel_us_mean": round(k_mean, 3), "bytes_per_launch": link,
                 "what": "cold-page bytes read over the host link (PCIe 5.0 x16, 64 GB/s a direction)",
-                "node": {"us": round(us, 3), "achieved": round(node, 1),
-                         "frac": round(node / HOST_LINK_PEAK_GBS, 4)}}, "window_lossless")
+                "node_us": round(us, 3), "node_achieved": round(node, 1),
+                "node_frac": round(node / HOST_LINK_PEAK_GBS, 4)}, "window_lossless")
             hb = (hbm + qo) / (k_mean * 1e-6) / 1e9
             entry["roofline_hbm"] = {"bound": "hbm", "achieved": round(hb, 1), "peak": HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(hb / HBM_PEAK_GBS, 4),
@@ -956,6 +979,83 @@ def cpu_leg(run, unit: str, scale_us: float, sample: str, budget_s: float, run_1
     return res
 
 
+def _g(d, *path):
+    for p in path:
+        if not isinstance(d, dict) or p not in d:
+            return None
+        d = d[p]
+    return d
+
+
+def _traffic_x(roof):
+    """HBM traffic per launch over the algorithmic bytes (or None)."""
+    t, b = _g(roof, "traffic"), _g(roof, "bytes_per_launch")
+    return round(t / b, 3) if t and b else None
+
+
+def decode_fields(prefix: str, leg: dict, per: str = "us_per_layer_token") -> dict:
+    roof = _g(leg, "roofline") or {}
+    return {f"{prefix}_us": _g(leg, per), f"{prefix}_kernel_us": roof.get("kernel_us_mean"),
+            f"{prefix}_frac": roof.get("frac"), f"{prefix}_rocprof_frac": roof.get("rocprof_frac"),
+            f"{prefix}_node_frac": roof.get("node_frac"), f"{prefix}_traffic_x": _traffic_x(roof),
+            f"{prefix}_cpu_us": _g(leg, "cpu_baseline", "value"),
+            f"{prefix}_cpu_us_1t": _g(leg, "cpu_baseline", "value_1_thread")}
+
+
+def legs_summary(r: dict) -> dict:
+    """Every workload's headline figures in one flat object (printed last on
+    the line): µs, roofline fractions (live HIP events / rocprof mean / whole
+    node), HBM traffic over algorithmic bytes, and the CPU oracle at all
+    allotted threads and at one thread."""
+    s = {"decode_f16_4k_us": r.get("value"), "decode_f16_4k_kernel_us": _g(r, "roofline", "kernel_us_mean"),
+         "decode_f16_4k_frac": _g(r, "roofline", "frac"),
+         "decode_f16_4k_rocprof_frac": _g(r, "roofline", "rocprof_frac"),
+         "decode_f16_4k_node_frac": _g(r, "roofline", "node_frac"),
+         "decode_f16_4k_traffic_x": _traffic_x(r.get("roofline")),
+         "decode_f16_4k_cpu_us": _g(r, "cpu_baseline", "value"),
+         "decode_f16_4k_cpu_us_1t": _g(r, "cpu_baseline", "value_1_thread")}
+    if "f16_ctx32k" in r:
+        s.update(decode_fields("decode_f16_32k", r["f16_ctx32k"]))
+    q8 = r.get("q8_0") or {}
+    if q8:
+        s.update(decode_fields("decode_q8_0_32k_b1", q8.get("ctx32k_b1")))
+        s.update(decode_fields("decode_q8_0_b8", q8.get("b8_varlen_8k_32k"), per="us_per_layer_step"))
+    pf = r.get("prefill") or {}
+    if pf:
+        s.update({"prefill_f16_us": pf.get("us_per_layer_chunk"), "prefill_f16_frac": pf.get("frac"),
+                  "prefill_f16_rocprof_frac": pf.get("rocprof_frac"),
+                  "prefill_f16_mfma_busy": pf.get("rocprof_mfma_busy"),
+                  "prefill_f16_cpu_us": pf.get("cpu_value"), "prefill_f16_cpu_us_1t": pf.get("cpu_value_1_thread")})
+    for name, leg in (("prefill_q8_0", _g(q8, "prefill_2048_on_2048")),
+                      ("prefill_f32", _g(r, "f32", "prefill_2048_on_2048"))):
+        if leg:
+            s.update({f"{name}_us": leg.get("us_per_layer_chunk"), f"{name}_frac": leg.get("frac"),
+                      f"{name}_rocprof_frac": leg.get("rocprof_frac")})
+    if _g(r, "f32", "decode_ctx4096"):
+        s.update(decode_fields("decode_f32_4k", r["f32"]["decode_ctx4096"]))
+    w = r.get("window") or {}
+    if w.get("sliding_window"):
+        s.update(decode_fields("window_sliding_b4", w["sliding_window"], per="us_per_layer_step"))
+        s["window_sliding_b4_steps"] = w["sliding_window"].get("steps")
+    if w.get("lossless"):
+        s.update(decode_fields("window_lossless_b4", w["lossless"], per="us_per_layer_step"))
+        s["window_lossless_b4_steps"] = w["lossless"].get("steps")
+        s["window_lossless_b4_bound"] = _g(w, "lossless", "roofline", "bound")
+    ra = r.get("rope_append") or {}
+    if ra:
+        s.update({"rope_append_b1_us": _g(ra, "decode_b1", "us_per_layer_token"),
+                  "rope_append_2048_us": _g(ra, "prefill_2048", "us_per_layer_chunk"),
+                  "rope_append_2048_frac": _g(ra, "prefill_2048", "roofline", "frac")})
+    wo = r.get("decode_wo") or {}
+    if wo:
+        s.update({"decode_wo_fused_us": wo.get("us_per_layer_token"),
+                  "decode_wo_unfused_us": wo.get("us_per_layer_token_unfused_sfa")})
+    ly = r.get("decode_layer") or {}
+    if ly:
+        s.update({"layer_us": ly.get("us_per_layer_token"), "layer_frac": _g(ly, "roofline", "frac")})
+    return {k: v for k, v in s.items() if v is not None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -966,8 +1066,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-budget", type=float, default=4.0, metavar="S",
                     help="seconds of timed CPU work per thread count and CPU leg")
-    ap.add_argument("--window-lossless-steps", type=int, default=8, metavar="N",
+    ap.add_argument("--window-lossless-steps", type=int, default=128, metavar="N",
                     help="decode steps of the lossless window leg (N-1 timed)")
+    ap.add_argument("--window-lossless-layers", type=int, default=4, metavar="L",
+                    help="layers of the lossless window leg")
     ap.add_argument("--window-steps", type=int, default=128, metavar="N",
                     help="decode steps of the sliding-window leg (N-1 timed)")
     ap.add_argument("--no-prefill", action="store_true")
@@ -1027,7 +1129,8 @@ def main():
             r = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
         else:
             r = window_bench(torch, args.seed + 3, steps=args.window_steps,
-                             lossless_steps=args.window_lossless_steps)
+                             lossless_steps=args.window_lossless_steps,
+                             lossless_layers=args.window_lossless_layers)
         print(json.dumps({args.only: r}))
         return
 
@@ -1085,6 +1188,7 @@ def main():
     if not args.no_window:
         result["window"] = window_bench(torch, args.seed + 3, steps=args.window_steps,
                                         lossless_steps=args.window_lossless_steps,
+                                        lossless_layers=args.window_lossless_layers,
                                         cpu_budget_s=cpu_s)
     if not args.no_rope:
         result["rope_append"] = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
@@ -1095,6 +1199,24 @@ def main():
     if not args.no_layer:
         result["decode_layer"] = layer_bench(torch, max(args.steps // 5, 5), 2, args.seed + 8)
     result["hbm_copy_ceiling"] = copy_ceiling(torch)
+    # the decode legs at 32k beside the headline roofline, the other prefill
+    # caches beside the f16 prefill (flat fields)
+    roof = result["roofline"]
+    for prefix, leg in (("f16_ctx32k", result.get("f16_ctx32k")),
+                        ("q8_0_ctx32k_b1", _g(result, "q8_0", "ctx32k_b1")),
+                        ("q8_0_b8", _g(result, "q8_0", "b8_varlen_8k_32k"))):
+        if leg:
+            roof[f"{prefix}_frac"] = _g(leg, "roofline", "frac")
+            roof[f"{prefix}_rocprof_frac"] = _g(leg, "roofline", "rocprof_frac")
+            roof[f"{prefix}_kernel_us"] = _g(leg, "roofline", "kernel_us_mean")
+    pf = result.get("prefill")
+    if pf:
+        for prefix, leg in (("q8_0", _g(result, "q8_0", "prefill_2048_on_2048")),
+                            ("f32", _g(result, "f32", "prefill_2048_on_2048"))):
+            if leg:
+                pf[f"{prefix}_us_per_layer_chunk"] = leg.get("us_per_layer_chunk")
+                pf[f"{prefix}_frac"] = leg.get("frac")
+    result["legs"] = legs_summary(result)
     print(json.dumps(result))
 
 

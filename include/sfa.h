@@ -69,7 +69,7 @@ extern "C" {
 typedef struct sfa_kv_desc {
     int32_t n_head;        /* Hq (query heads)                                  */
     int32_t n_head_kv;     /* Hkv; n_head % n_head_kv == 0                      */
-    int32_t head_dim;      /* 32, 64 or 128                                     */
+    int32_t head_dim;      /* 32, 64 or 128 (64 or 128 for SFA_KV_Q8_0)         */
     int32_t page_size;     /* positions per page, a multiple of 32              */
     int32_t kv_type;       /* SFA_KV_F32, SFA_KV_F16 or SFA_KV_Q8_0             */
     int32_t n_pages;       /* pages in k_pages / v_pages                        */

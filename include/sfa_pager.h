@@ -42,8 +42,9 @@ typedef struct sfa_pager_config {
     int32_t n_layer;
     int32_t n_head, n_head_kv, head_dim;
     int32_t kv_type;       /* SFA_KV_F32, SFA_KV_F16 or SFA_KV_Q8_0                  */
-    int32_t page_size;     /* positions per page, a multiple of 32 (of 64 for steps  */
-                           /* of more than one token per sequence: the prefill)     */
+    int32_t page_size;     /* positions per page, a multiple of 64 (a multi-token    */
+                           /* step is attended by the prefill's 64-position tiles); */
+                           /* other sizes: SFA_ERR_UNSUPPORTED from create          */
     int32_t n_seq;         /* sequences decoded together                             */
     int32_t n_ctx;         /* positions per sequence (KvStore capacity)              */
     int32_t window;        /* resident positions per sequence; 0 = n_ctx (no paging) */
@@ -99,8 +100,8 @@ SFA_API int sfa_pager_rope_append(sfa_pager *pager, int32_t layer, float *q, con
  * f32 device, out [n_tokens][n_head * head_dim] f32 device.  A step with one
  * token per sequence runs sfa_attn_decode over the batch (split plan sized for
  * n_ctx when lossless, `window` when windowed); other steps run
- * sfa_attn_prefill per sequence with tokens (its limits: page_size a multiple
- * of 64, Q8_0 with head_dim >= 64; otherwise SFA_ERR_UNSUPPORTED).  Under
+ * sfa_attn_prefill per sequence with tokens (its page-size and Q8_0 head_dim
+ * limits are checked by sfa_pager_create already).  Under
  * SFA_ATTEND_WINDOW a sequence may take at most one token in such a step (each
  * token of a chunk would need its own window start): SFA_ERR_UNSUPPORTED. */
 SFA_API int sfa_pager_attend(sfa_pager *pager, int32_t layer, const float *q, float *out,

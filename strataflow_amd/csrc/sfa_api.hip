@@ -43,6 +43,11 @@ int check_desc(const sfa_kv_desc *kv) {
     if (kv->page_size <= 0 || kv->page_size % sfa::kTile != 0) return SFA_ERR_INVALID_ARGUMENT;
     if (kv->kv_type != SFA_KV_F32 && kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_Q8_0)
         return SFA_ERR_UNSUPPORTED;
+    // the Q8_0 attention kernels take two or four 32-element blocks per row
+    // (one per lane half); a one-block row (head_dim 32) is refused for every
+    // entry point, the append included, so no cache is written that nothing
+    // could attend over
+    if (kv->kv_type == SFA_KV_Q8_0 && kv->head_dim < 64) return SFA_ERR_UNSUPPORTED;
     if (kv->n_pages < 0 || kv->n_cold_pages < 0) return SFA_ERR_INVALID_ARGUMENT;
     if (kv->n_pages > 0 && (kv->k_pages == nullptr || kv->v_pages == nullptr))
         return SFA_ERR_INVALID_ARGUMENT;

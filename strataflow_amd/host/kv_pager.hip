@@ -235,6 +235,9 @@ SFA_API int sfa_pager_create(const sfa_pager_config *cfg_in, sfa_pager **out) {
     sfa_pager_config c = *cfg_in;
     if (c.n_layer <= 0 || c.n_seq <= 0 || c.n_ctx <= 0 || c.page_size <= 0 || c.window < 0)
         return SFA_ERR_INVALID_ARGUMENT;
+    // a multi-token step is attended by the chunked prefill, whose 64-position
+    // tiles must not straddle a page: refused here, before any step is begun
+    if (c.page_size % 64 != 0) return SFA_ERR_UNSUPPORTED;
     if (c.attend != SFA_ATTEND_LOSSLESS && c.attend != SFA_ATTEND_WINDOW)
         return SFA_ERR_INVALID_ARGUMENT;
     if (c.window == 0 || c.window > c.n_ctx) c.window = c.n_ctx;

@@ -91,18 +91,42 @@ def test_desc_check_rejects(field, value, status):
     assert lib.sfa_kv_desc_check(ctypes.byref(desc(**{field: value}))) == status
 
 
-def test_q8_0_head_dim_32_is_unsupported_for_attention():
-    """A Q8_0 cache with head_dim 32 is appended to (the RoPE + append kernel
-    takes it) but not attended over: decode and prefill return
-    SFA_ERR_UNSUPPORTED from their host checks, before any device work."""
+def test_q8_0_head_dim_32_is_unsupported():
+    """A Q8_0 cache with head_dim 32 (one block per row) is refused by the
+    descriptor check, so every entry point over it returns
+    SFA_ERR_UNSUPPORTED from the host, before any device work: the append and
+    the fused RoPE + append as well as decode and prefill (a cache that nothing
+    could attend over is never written)."""
     lib = _lib.load()
     d = desc(kv_type=_lib.SFA_KV_Q8_0, head_dim=32)
-    assert lib.sfa_kv_desc_check(ctypes.byref(d)) == _lib.SFA_OK
+    uns = _lib.SFA_ERR_UNSUPPORTED
+    assert lib.sfa_kv_desc_check(ctypes.byref(d)) == uns
+    assert lib.sfa_kv_desc_check(ctypes.byref(desc(kv_type=_lib.SFA_KV_Q8_0, head_dim=64))) == _lib.SFA_OK
     p = 0x1000  # never dereferenced
-    ws = lib.sfa_decode_workspace_bytes(ctypes.byref(d), 1, 256)
-    assert lib.sfa_attn_decode(ctypes.byref(d), p, p, p, 4, p, None, 1, 256, 0.1, p, ws,
-                               None) == _lib.SFA_ERR_UNSUPPORTED
-    assert lib.sfa_attn_prefill(ctypes.byref(d), p, p, p, 4, 0, 16, 0, 0.1, None) == _lib.SFA_ERR_UNSUPPORTED
+    assert lib.sfa_kv_append(ctypes.byref(d), p, p, p, p, 4, p, 4, None) == uns
+    assert lib.sfa_rope_kv_append(ctypes.byref(d), p, p, p, p, p, 4, p, 4, 1e4, None) == uns
+    assert lib.sfa_decode_workspace_bytes(ctypes.byref(d), 1, 256) == 0
+    assert lib.sfa_attn_decode(ctypes.byref(d), p, p, p, 4, p, None, 1, 256, 0.1, p, 1 << 20,
+                               None) == uns
+    assert lib.sfa_attn_prefill(ctypes.byref(d), p, p, p, 4, 0, 16, 0, 0.1, None) == uns
+
+
+@pytest.mark.parametrize("page_size", [32, 96, 100])
+def test_pager_refuses_page_sizes_the_prefill_cannot_tile(page_size):
+    """A pager attends multi-token steps with the chunked prefill, whose
+    64-position tiles must not straddle a page: sfa_pager_create refuses a
+    page size that is not a multiple of 64 up front (host check, before any
+    allocation), instead of refusing the attention after a step has begun."""
+    lib = _lib.load_host()
+    c = _lib.SfaPagerConfig(2, 32, 8, 128, _lib.SFA_KV_F16, page_size, 2, 2048, 300,
+                            _lib.SFA_ATTEND_LOSSLESS, 0, 0, 0)
+    h = ctypes.c_void_p()
+    assert lib.sfa_pager_create(ctypes.byref(c), ctypes.byref(h)) == _lib.SFA_ERR_UNSUPPORTED
+    assert not h.value
+    # a Q8_0 cache of head_dim 32 is refused by the pager's shape check too
+    c = _lib.SfaPagerConfig(2, 8, 4, 32, _lib.SFA_KV_Q8_0, 256, 2, 2048, 300,
+                            _lib.SFA_ATTEND_LOSSLESS, 0, 0, 0)
+    assert lib.sfa_pager_create(ctypes.byref(c), ctypes.byref(h)) == _lib.SFA_ERR_UNSUPPORTED
 
 
 def test_page_table_check():

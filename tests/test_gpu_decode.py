@@ -337,15 +337,16 @@ def test_decode_one_sequence_many_splits(gpu, oracle_mod, kv_type, shape, n_kv):
     # one sequence whose kv-head rows have 65 .. 256 split records (few kv
     # heads, long context): the wide merge pass
     Hq, Hkv, hd = shape
-    c = Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=kv_type,
-             seed=n_kv + Hkv)
     if kv_type == 8 and hd < 64:
-        # Q8_0 attention needs head_dim >= 64: the call is refused, not run
+        # a Q8_0 cache of head_dim 32 is refused for every entry point
         from strataflow_amd import _lib
         with pytest.raises(_lib.SfaError) as e:
-            c.decode()
+            Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=kv_type,
+                 seed=n_kv + Hkv)
         assert e.value.status == _lib.SFA_ERR_UNSUPPORTED
         return
+    c = Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=kv_type,
+             seed=n_kv + Hkv)
     out = c.decode()
     if kv_type == 8:
         assert_close(out, c.oracle(oracle_mod.GGML), what=f"q8 {shape} n_kv={n_kv} vs ggml")

@@ -25,6 +25,13 @@ def test_append_bit_exact(gpu, oracle_mod, kv_type, hd):
     v = rng.standard_normal((n_tok, Hkv, hd)).astype(np.float32)
     k[5, 1, :32] = 0.0
     v[7, 0, :32] = 1e4
+    if kv_type == 8 and hd < 64:
+        # a Q8_0 cache of head_dim 32 is refused for every entry point
+        from strataflow_amd import _lib
+        with pytest.raises(_lib.SfaError) as e:
+            PagedKV(1, Hkv, Hkv, hd, kv_type, ps, n_pages, device=gpu)
+        assert e.value.status == _lib.SFA_ERR_UNSUPPORTED
+        return
     host = oracle_mod.HostPagedKv(Hkv, hd, ps, kv_type, n_pages)
     assert host.append(k, v, seq, pos, pt) == 0
     dev = PagedKV(1, Hkv, Hkv, hd, kv_type, ps, n_pages, device=gpu)
