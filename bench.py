@@ -408,93 +408,14 @@ def prefill_bench(torch, steps: int, warmup: int, seed: int, kv_type: int = 1, c
     return res
 
 
-def decode_wo_bench(torch, steps: int, warmup: int, seed: int):
-    """The decode node with its consumer fused in (sfa_attn_decode_wo):
-    y = wo @ attn + residual, wo f16 [4096, 4096] per layer (the Mixtral
-    attn_output.weight shape), B=1, context 4096, 32 layers with distinct caches
-    and weights, graph-replayed.  Beside it two unfused chains: the decode node,
-    then the projection and the residual add as torch ops (f16 GEMV, casts,
-    add), or as one sfa_mul_mat_vec pass."""
-    n_embd = HQ * HD
-    kv, pt, t_pt, q, seq_len = build_decode_workload(torch, 4096, seed)
-    dev = q.device
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(seed)
-    wo = [(torch.randn((n_embd, HQ * HD), device=dev, generator=gen) / math.sqrt(HQ * HD)).half()
-          for _ in range(N_LAYER)]
-    x = torch.randn((N_LAYER, 1, n_embd), device=dev, generator=gen)
-    y = torch.empty_like(x)
-    attn = torch.empty((N_LAYER, 1, HQ * HD), device=dev)
-
-    def fused():
-        for layer in range(N_LAYER):
-            kv.decode_wo(layer, q[layer], t_pt, seq_len, 4096, wo[layer], x[layer], y=y[layer])
-
-    def unfused():
-        for layer in range(N_LAYER):
-            kv.decode(layer, q[layer], t_pt, seq_len, 4096, out=attn[layer])
-            y[layer] = torch.nn.functional.linear(attn[layer].half(), wo[layer]).float() + x[layer]
-
-    from strataflow_amd import layer as ops
-
-    def unfused_sfa():
-        for layer in range(N_LAYER):
-            kv.decode(layer, q[layer], t_pt, seq_len, 4096, out=attn[layer])
-            ops.mul_mat_vec(wo[layer], attn[layer], residual=x[layer], out=y[layer])
-
-    res = {}
-    for name, fn in (("fused", fused), ("unfused", unfused), ("unfused_sfa", unfused_sfa)):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            fn()
-        for _ in range(warmup):
-            g.replay()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(steps):
-            g.replay()
-        b.record()
-        torch.cuda.synchronize()
-        res[name] = a.elapsed_time(b) * 1e3 / (steps * N_LAYER)
-        del g
-    alg = 2 * 4096 * HKV * HD * 2 + HQ * HD * 4 + n_embd * HQ * HD * 2 + 2 * n_embd * 4
-    ach = alg / (res["fused"] * 1e-6) / 1e9
-    out = {
-        "workload": "decode-attn f16 KV + output projection (wo f16 [4096, 4096]) + residual, Mixtral GQA "
-                    "32q/8kv hd128, B=1, context 4096, 32 layers with distinct caches and weights",
-        "us_per_layer_token": round(res["fused"], 3),
-        "us_per_layer_token_unfused": round(res["unfused"], 3),
-        "unfused": "sfa_attn_decode, then torch f16 linear + cast + residual add",
-        "us_per_layer_token_unfused_sfa": round(res["unfused_sfa"], 3),
-        "unfused_sfa": "sfa_attn_decode, then sfa_mul_mat_vec (f16 wo, residual added in the same pass)",
-        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "split-K pass + merge_wo_kernel<128,4,f16> (the node, graph-replayed)",
-                     "bytes_per_launch": alg,
-                     "what": "K + V + Q + wo + residual + y once, over the node's time"},
-        # the fused second pass alone: wo once, the split records once, residual in, y out
-        "merge_wo_kernel": with_traffic({"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                         "frac": None, "traffic": None,
-                                         "kernel": "merge_wo_kernel<128,4,f16,true>",
-                                         "bytes_per_launch": n_embd * HQ * HD * 2 + HKV * 32 * 4 * (HD + 4) * 4
-                                         + 2 * n_embd * 4}, "decode_wo_f16"),
-    }
-    del kv, q, wo
-    torch.cuda.empty_cache()
-    return out
-
-
 def layer_bench(torch, steps: int, warmup: int, seed: int, n_layer: int = 8) -> dict:
     """The whole decode layer on the GPU: n_layer Mixtral-shaped layers (n_embd
     4096, 32 q / 8 kv heads of 128, 8 experts top-2, n_ff 14336; f16 weights
     N(0,1)*0.02, distinct per layer) over distinct f16 caches at context 4096,
     B = 1, one token per step through every layer, the step captured as one HIP
     graph: rms_norm, the Q/K/V product (the three weights stacked), fused RoPE
-    + KV append, attention with wo + residual fused, rms_norm, the router
+    + KV append, attention, the wo product with the residual added in the same
+    pass, rms_norm, the router
     product, routing, the two routed experts' SwiGLU FFN and the residual.
     The roofline counts the bytes a layer-token reads once: the Q/K/V, wo and
     router weights, the two routed experts' gate, up and down rows, the KV
@@ -537,47 +458,40 @@ def layer_bench(torch, steps: int, warmup: int, seed: int, n_layer: int = 8) -> 
 
     attn = torch.empty((1, HQ * HD), device=dev)
 
-    def step(fused_wo: bool):
+    def step():
         x.copy_(x0)
         for il, L in enumerate(layers):
             ops.rms_norm(x, L["attn_norm"], 1e-5, out=cur)
             ops.mul_mat_vec(L["wqkv"], cur, out=qkv)
             kv.rope_append(il, q, k, v, seq1, pos1, pt, 1e6)
-            if fused_wo:
-                kv.decode_wo(il, q, pt, sl, ctx, L["wo"], x, y=ffn_inp)
-            else:
-                kv.decode(il, q, pt, sl, ctx, out=attn)
-                ops.mul_mat_vec(L["wo"], attn, residual=x, out=ffn_inp)
+            kv.decode(il, q, pt, sl, ctx, out=attn)
+            ops.mul_mat_vec(L["wo"], attn, residual=x, out=ffn_inp)
             ops.rms_norm(ffn_inp, L["ffn_norm"], 1e-5, out=cur)
             ops.moe_gate(L["gate_inp"], cur, K, ids=ids, weights=wts)
             ops.moe_ffn(cur, ffn_inp, ids, wts, L["gate"], L["up"], L["down"], out=x, workspace=moe_ws)
 
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    res = {}
-    for fused in (True, False):
-        step(fused)
-        torch.cuda.synchronize()
-        a.record()
-        for _ in range(3):
-            step(fused)
-        b.record()
-        torch.cuda.synchronize()
-        eager_us = a.elapsed_time(b) * 1e3 / (3 * n_layer)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step(fused)
-        for _ in range(warmup):
-            g.replay()
-        torch.cuda.synchronize()
-        a.record()
-        for _ in range(steps):
-            g.replay()
-        b.record()
-        torch.cuda.synchronize()
-        res[fused] = (a.elapsed_time(b) * 1e3 / (steps * n_layer), eager_us)
-        del g
-    fused_best = res[True][0] <= res[False][0]
-    us, eager_us = res[fused_best]
+    step()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(3):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    eager_us = a.elapsed_time(b) * 1e3 / (3 * n_layer)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / (steps * n_layer)
+    del g
     out_ok = bool(torch.isfinite(x).all().item())
     routed = ids.cpu().numpy().tolist()
     alg = (2 * ((HQ + 2 * HKV) * HD * D + D * HQ * HD + E * D)      # Q/K/V, wo, router weights (f16)
@@ -594,9 +508,6 @@ def layer_bench(torch, steps: int, warmup: int, seed: int, n_layer: int = 8) -> 
         "us_per_layer_token": round(us, 2),
         "us_per_layer_token_eager": round(eager_us, 2),
         "tokens_per_s_32_layers": round(1e6 / (us * 32), 1),
-        "attention_wo": "sfa_attn_decode_wo (fused)" if fused_best else "sfa_attn_decode + sfa_mul_mat_vec(wo, residual)",
-        "us_per_layer_token_fused_wo": round(res[True][0], 2),
-        "us_per_layer_token_unfused_wo": round(res[False][0], 2),
         "routed_experts_last_layer": routed,
         "finite": out_ok,
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -1046,10 +957,6 @@ def legs_summary(r: dict) -> dict:
         s.update({"rope_append_b1_us": _g(ra, "decode_b1", "us_per_layer_token"),
                   "rope_append_2048_us": _g(ra, "prefill_2048", "us_per_layer_chunk"),
                   "rope_append_2048_frac": _g(ra, "prefill_2048", "roofline", "frac")})
-    wo = r.get("decode_wo") or {}
-    if wo:
-        s.update({"decode_wo_fused_us": wo.get("us_per_layer_token"),
-                  "decode_wo_unfused_us": wo.get("us_per_layer_token_unfused_sfa")})
     ly = r.get("decode_layer") or {}
     if ly:
         s.update({"layer_us": ly.get("us_per_layer_token"), "layer_frac": _g(ly, "roofline", "frac")})
@@ -1078,10 +985,8 @@ def main():
     ap.add_argument("--no-32k", action="store_true", help="skip the f16 context-32768 decode leg")
     ap.add_argument("--no-rope", action="store_true", help="skip the fused RoPE + append leg")
     ap.add_argument("--no-f32", action="store_true", help="skip the F32-cache legs")
-    ap.add_argument("--no-wo", action="store_true", help="skip the fused output-projection leg")
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-decode-layer leg")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope", "f32", "wo",
-                                       "layer"],
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "q8", "prefill", "window", "rope", "f32", "layer"],
                     help="run one leg only and print its JSON (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB megabytes (HBM counter calibration)")
@@ -1111,7 +1016,7 @@ def main():
 
     if args.only == "decode4k":
         args.no_prefill = args.no_q8 = args.no_window = args.no_32k = args.no_cpu = args.no_rope = True
-        args.no_f32 = args.no_wo = args.no_layer = True
+        args.no_f32 = args.no_layer = True
     if args.only and args.only != "decode4k":
         if args.only == "decode32k":
             r = decode_leg(torch, "decode_f16_ctx32k", [32768], 1, max(args.steps // 4, 5), 3, args.seed + 4)
@@ -1125,8 +1030,6 @@ def main():
             r = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
         elif args.only == "layer":
             r = layer_bench(torch, max(args.steps // 5, 5), 2, args.seed + 8)
-        elif args.only == "wo":
-            r = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
         else:
             r = window_bench(torch, args.seed + 3, steps=args.window_steps,
                              lossless_steps=args.window_lossless_steps,
@@ -1194,8 +1097,6 @@ def main():
         result["rope_append"] = rope_bench(torch, max(args.steps // 5, 5), args.seed + 5)
     if not args.no_f32:
         result["f32"] = f32_bench(torch, max(args.steps // 4, 5), 3, args.seed + 6)
-    if not args.no_wo:
-        result["decode_wo"] = decode_wo_bench(torch, max(args.steps // 2, 5), 3, args.seed + 7)
     if not args.no_layer:
         result["decode_layer"] = layer_bench(torch, max(args.steps // 5, 5), 2, args.seed + 8)
     result["hbm_copy_ceiling"] = copy_ceiling(torch)

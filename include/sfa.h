@@ -184,8 +184,10 @@ SFA_API int sfa_attn_decode_merge(const sfa_kv_desc *kv, const float *q, float *
  * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
  * the reference (its attention is one ggml graph whose allocator owns every
  * buffer).  The split partials live in a library-owned device array of
- * SFA_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU
- * until the process ends; its address is looked up once per device.  The call
+ * SFA_NOALLOC_SCRATCH_BYTES per GPU: a global of libsfa's code object, so
+ * every process that loads libsfa's kernels on a GPU holds it there until the
+ * process ends, whether or not it calls this entry point; its address is
+ * looked up once per device, at the first call on that device.  The call
  * makes no allocation.  Returns SFA_ERR_OUT_OF_MEMORY when the shape needs
  * more than SFA_NOALLOC_SCRATCH_BYTES (sfa_decode_workspace_bytes tells the
  * need).  Every call on one GPU shares that GPU's array: calls that overlap
@@ -198,32 +200,6 @@ SFA_API int sfa_attn_decode_noalloc(const sfa_kv_desc *kv, const float *q, float
                                     const int32_t *page_table, int32_t max_pages,
                                     const int32_t *seq_len, const int32_t *kv_lo,
                                     int32_t B, int32_t max_seq_len, float scale, void *stream);
-
-/* Decode attention with its consumer fused in: y = wo * attn + residual, the
- * output projection and residual add after build_kv_attention
- * (src/model/engine/engine.cpp:1904-1906: cur = ggml_mul_mat(wo, attn_out);
- * ffn_inp = ggml_add(cur, inpSA)).  Arguments as sfa_attn_decode, plus
- *   wo       : [n_embd][n_head * head_dim] device, row r = output r (the ggml
- *              attn_output.weight layout, ne0 = n_head * head_dim), element type
- *              wo_type = SFA_KV_F32 or SFA_KV_F16 (ggml type ids); with F16
- *              weights the attention output is rounded to f16 before the dot
- *              products (ggml's vec_dot_type conversion), which accumulate in f32
- *   residual : [B][n_embd] f32 (inpSA);  y : [B][n_embd] f32 (ffn_inp)
- * The attention output is not written: the merge of the split-K partials
- * feeds the projection inside one pass (its values equal sfa_attn_decode's bit
- * for bit), and the kv heads' partial sums are added in a fixed order.  The
- * workspace (sfa_decode_wo_workspace_bytes) must be zeroed once before its
- * first use (sfa_workspace_init): it holds arrival counters that every call
- * leaves at zero.  Needs (n_head / n_head_kv) * head_dim >= 64. */
-SFA_API size_t sfa_decode_wo_workspace_bytes(const sfa_kv_desc *kv, int32_t B,
-                                             int32_t max_seq_len, int32_t n_embd);
-SFA_API int sfa_attn_decode_wo(const sfa_kv_desc *kv, const float *q,
-                               const int32_t *page_table, int32_t max_pages,
-                               const int32_t *seq_len, const int32_t *kv_lo,
-                               int32_t B, int32_t max_seq_len, float scale,
-                               const void *wo, int32_t wo_type, int32_t n_embd,
-                               const float *residual, float *y,
-                               void *workspace, size_t ws_bytes, void *stream);
 
 /* Chunked causal prefill of ONE sequence: T query tokens at absolute positions
  * q_pos0 .. q_pos0+T-1, whose K/V are already appended.  Token t attends kv

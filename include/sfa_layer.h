@@ -3,14 +3,14 @@
  * node (libsfa.so): the ops of build_router_segment and build_expert_segment
  * (src/model/engine/engine.cpp:1877-1925, 1945-1986 of the reference) on the
  * GPU, so a whole layer runs without a host round trip.  With sfa.h's
- * sfa_rope_kv_append, sfa_attn_decode / sfa_attn_prefill and
- * sfa_attn_decode_wo they cover the layer:
+ * sfa_rope_kv_append and sfa_attn_decode / sfa_attn_prefill they cover the
+ * layer:
  *
  *   cur     = rms_norm(x) * attn_norm         sfa_rms_norm            engine.cpp:1879-1880
  *   Q, K, V = Wq/Wk/Wv * cur                  sfa_mul_mat_vec         engine.cpp:1883-1885
  *   RoPE, KV append, attention                sfa.h                   engine.cpp:1892-1901
- *   ffn_inp = Wo * attn + x                   sfa_mul_mat_vec (or sfa_attn_decode_wo)
- *                                                                     engine.cpp:1905-1906
+ *   ffn_inp = Wo * attn + x                   sfa_mul_mat_vec         engine.cpp:1905-1906
+ *             (the residual added in the same pass)
  *   cur     = rms_norm(ffn_inp) * ffn_norm    sfa_rms_norm            engine.cpp:1908-1909
  *   logits  = gate_inp * cur                  sfa_mul_mat_vec         engine.cpp:1912
  *   ids, w  = top-k of softmax, renormalised  sfa_moe_route           engine.cpp:1913-1925

@@ -39,8 +39,6 @@ EXPORTS = (
     "sfa_attn_decode_split",
     "sfa_attn_decode_merge",
     "sfa_attn_decode_noalloc",
-    "sfa_decode_wo_workspace_bytes",
-    "sfa_attn_decode_wo",
     "sfa_attn_prefill",
     "sfa_page_table_check",
 )
@@ -124,11 +122,6 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         f.restype = ctypes.c_int
     lib.sfa_attn_decode_noalloc.argtypes = [D, P, P, P, i32, P, P, i32, i32, ctypes.c_float, P]
     lib.sfa_attn_decode_noalloc.restype = ctypes.c_int
-    lib.sfa_decode_wo_workspace_bytes.argtypes = [D, i32, i32, i32]
-    lib.sfa_decode_wo_workspace_bytes.restype = ctypes.c_size_t
-    lib.sfa_attn_decode_wo.argtypes = [D, P, P, i32, P, P, i32, i32, ctypes.c_float, P, i32, i32, P, P, P,
-                                       ctypes.c_size_t, P]
-    lib.sfa_attn_decode_wo.restype = ctypes.c_int
     lib.sfa_attn_prefill.argtypes = [D, P, P, P, i32, i32, i32, i32, ctypes.c_float, P]
     lib.sfa_attn_prefill.restype = ctypes.c_int
     lib.sfa_page_table_check.argtypes = [D, P, i32, P, P, i32]

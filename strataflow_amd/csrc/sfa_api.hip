@@ -23,11 +23,6 @@ int rope_append_launch(const sfa_kv_desc *kv, float *q, const float *k, const fl
                        const int32_t *page_table, int32_t max_pages, float freq_base,
                        hipStream_t stream);
 int workspace_init_launch(void *ws, size_t bytes, hipStream_t stream);
-size_t decode_wo_workspace_bytes(const sfa_kv_desc *kv, int B, int max_seq_len, int n_embd);
-int decode_wo_launch(const sfa_kv_desc *kv, const float *q, const int32_t *page_table, int32_t max_pages,
-                     const int32_t *seq_len, const int32_t *kv_lo, int32_t B, int32_t max_seq_len,
-                     float scale, const void *wo, int32_t wo_type, int32_t n_embd, const float *residual,
-                     float *y, void *workspace, size_t ws_bytes, hipStream_t stream);
 int decode_noalloc_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
                           int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
                           int32_t max_seq_len, float scale, hipStream_t stream);
@@ -184,29 +179,6 @@ SFA_API int sfa_attn_decode_noalloc(const sfa_kv_desc *kv, const float *q, float
         if (!(scale > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
         return sfa::decode_noalloc_launch(kv, q, out, page_table, max_pages, seq_len, kv_lo, B,
                                           max_seq_len, scale, static_cast<hipStream_t>(stream));
-    } catch (...) {
-        return SFA_ERR_RUNTIME;
-    }
-}
-
-SFA_API size_t sfa_decode_wo_workspace_bytes(const sfa_kv_desc *kv, int32_t B, int32_t max_seq_len,
-                                             int32_t n_embd) {
-    if (check_desc(kv) != SFA_OK || B <= 0 || max_seq_len <= 0 || n_embd <= 0) return 0;
-    return sfa::decode_wo_workspace_bytes(kv, B, max_seq_len, n_embd);
-}
-
-SFA_API int sfa_attn_decode_wo(const sfa_kv_desc *kv, const float *q, const int32_t *page_table,
-                               int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo,
-                               int32_t B, int32_t max_seq_len, float scale, const void *wo,
-                               int32_t wo_type, int32_t n_embd, const float *residual, float *y,
-                               void *workspace, size_t ws_bytes, void *stream) {
-    try {
-        const int rc = check_desc(kv);
-        if (rc != SFA_OK) return rc;
-        if (!(scale > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
-        return sfa::decode_wo_launch(kv, q, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
-                                     wo, wo_type, n_embd, residual, y, workspace, ws_bytes,
-                                     static_cast<hipStream_t>(stream));
     } catch (...) {
         return SFA_ERR_RUNTIME;
     }

@@ -1,6 +1,5 @@
 // sfa_decode.h - the split-K decode's parameters and split plan, shared by
-// the decode passes (sfa_decode.hip) and the fused output projection
-// (sfa_decode_wo.hip).  Device helpers are inline; the host side of the plan
+// the decode passes (sfa_decode.hip).  Device helpers are inline; the host side of the plan
 // (split-row sizing, workspace size, parameter setup) is declared at the end.
 #pragma once
 

@@ -61,7 +61,6 @@ class PagedKV:
         else:
             self.k_cold = self.v_cold = None
         self._ws = None
-        self._ws_wo = None
         self._ws_need = {}
         self._descs = [self._make_desc(layer) for layer in range(n_layer)]
         lib = _lib.load()
@@ -159,42 +158,6 @@ class PagedKV:
             split_end_event.record()
             _lib.check(lib.sfa_attn_decode_merge(*args), "sfa_attn_decode_merge")
         return out
-
-    def decode_wo(self, layer: int, q: torch.Tensor, page_table: torch.Tensor, seq_len: torch.Tensor,
-                  max_seq_len: int, wo: torch.Tensor, residual: torch.Tensor,
-                  kv_lo: torch.Tensor | None = None, y: torch.Tensor | None = None,
-                  scale: float | None = None, stream=None) -> torch.Tensor:
-        """Decode with the output projection and residual fused in:
-        y [B, n_embd] = wo [n_embd, Hq*hd] (f32 or f16) @ attn + residual."""
-        B = int(seq_len.numel())
-        assert q.is_contiguous() and q.shape == (B, self.n_head, self.head_dim)
-        assert wo.is_contiguous() and wo.dim() == 2 and wo.shape[1] == self.n_head * self.head_dim
-        n_embd = int(wo.shape[0])
-        assert residual.is_contiguous() and residual.shape == (B, n_embd) and residual.dtype == torch.float32
-        wo_type = {torch.float32: SFA_KV_F32, torch.float16: SFA_KV_F16}[wo.dtype]
-        if y is None:
-            y = torch.empty((B, n_embd), dtype=torch.float32, device=q.device)
-        lib = _lib.load()
-        d = self._descs[layer]
-        key = ("wo", B, max_seq_len, n_embd)
-        need = self._ws_need.get(key)
-        if need is None:
-            need = lib.sfa_decode_wo_workspace_bytes(ctypes.byref(d), B, max_seq_len, n_embd)
-            if need == 0:
-                raise ValueError("invalid decode shape")
-            self._ws_need[key] = need
-        if self._ws_wo is None or self._ws_wo.numel() < need:
-            # the fused pass keeps arrival counters here: zeroed once, left at zero by every call
-            self._ws_wo = torch.empty(need, dtype=torch.uint8, device=self.device)
-            _lib.check(lib.sfa_workspace_init(self._ws_wo.data_ptr(), self._ws_wo.numel(), _stream(stream)),
-                       "workspace init")
-        _lib.check(lib.sfa_attn_decode_wo(ctypes.byref(d), q.data_ptr(), page_table.data_ptr(),
-                                          int(page_table.shape[1]), seq_len.data_ptr(), _ptr(kv_lo), B,
-                                          int(max_seq_len), float(scale if scale is not None else self.scale),
-                                          wo.data_ptr(), wo_type, n_embd, residual.data_ptr(), y.data_ptr(),
-                                          self._ws_wo.data_ptr(), self._ws_wo.numel(), _stream(stream)),
-                   "sfa_attn_decode_wo")
-        return y
 
     def prefill(self, layer: int, q: torch.Tensor, page_table: torch.Tensor, q_pos0: int,
                 kv_lo: int = 0, out: torch.Tensor | None = None, scale: float | None = None,

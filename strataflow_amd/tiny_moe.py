@@ -203,9 +203,9 @@ class TinyMoeGpu(TinyMoe):
     build_router_segment + build_expert_segment (engine.cpp:1877-1986) op by
     op: rms_norm * attn_norm; one product for Q, K and V (the three weights
     stacked row-wise: the same dot products, one launch); RoPE of Q and K fused
-    with the KV append; attention with the wo projection and the residual fused
-    in for one token (sfa_attn_decode_wo), or the causal prefill then the wo
-    product for a chunk; rms_norm * ffn_norm; the router product; softmax top-k
+    with the KV append; the decode (one token) or the causal prefill (a
+    chunk), then the wo product with the residual added in the same pass;
+    rms_norm * ffn_norm; the router product; softmax top-k
     routing; the SwiGLU experts with their weighted sum and the residual; the
     output head.  Token ids go in and the last row's logits come out; nothing
     else crosses the host link.  ``weight_dtype`` float16 rounds the weights
@@ -260,10 +260,10 @@ class TinyMoeGpu(TinyMoe):
             v = qkv[:, (Hq + Hkv) * hd:].contiguous().view(T, Hkv, hd)
             self.kv.rope_append(il, q, k, v, seq, pos, self.pt, cfg.freq_base)
             if T == 1:
-                ffn_inp = self.kv.decode_wo(il, q, self.pt, sl, self.n_ctx, L["wo"], x)
+                attn = self.kv.decode(il, q, self.pt, sl, self.n_ctx)
             else:
                 attn = self.kv.prefill(il, q, self.pt[0], pos0)
-                ffn_inp = ops.mul_mat_vec(L["wo"], attn, residual=x)
+            ffn_inp = ops.mul_mat_vec(L["wo"], attn, residual=x)
             cur = ops.rms_norm(ffn_inp, L["ffn_norm"], cfg.rms_eps)
             ids, wts = ops.moe_gate(L["gate_inp"], cur, cfg.n_expert_used)
             need = T * cfg.n_expert_used * cfg.n_ff * 4
