@@ -104,11 +104,15 @@ __device__ __attribute__((always_inline)) inline void prefill_mask(floatx16 (&s)
 // it by 2^8 (P stays <= 256; exact since O and l share the reference).
 // Returns the factor O and l are rescaled by (1 when the reference stays).
 __device__ __attribute__((always_inline)) inline float prefill_rescale(const floatx16 (&s)[2], float scale_log2, float &m_run) {
-    float mt = -INFINITY;
+    // a reduction tree (5 levels) rather than a 32-long dependent chain
+    float a[16];
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
+    for (int i = 0; i < 16; ++i) a[i] = fmaxf(s[0][i], s[1][i]);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[pb][i]);
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) a[i] = fmaxf(a[i], a[i + w]);
+    float mt = a[0];
     mt = fmaxf(mt, xor32(mt)) * scale_log2;
     float alpha = 1.0f;
     if (mt > m_run + kRescaleLog2) {
@@ -134,25 +138,62 @@ __device__ __attribute__((always_inline)) inline void prefill_write(const floatx
     }
 }
 
+// LDS address (32 bits) of a pointer into shared memory.
+__device__ inline uint32_t lds_u32(const void *ptr) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)(ptr);
+}
+
+// One 16-byte chunk per lane from a buffer resource straight into LDS
+// (buffer_load_dwordx4 ... lds): the instruction fills the 1 KB block at
+// lds_addr (wave-uniform), lane l its chunk l, from byte voff of the resource
+// (past num_records a lane reads zeros).  Issued from asm, so the compiler
+// does not count these loads: its own LDS reads of the other buffers do not
+// wait for them, and the caller waits with s_waitcnt vmcnt before the
+// barrier that publishes the tile.  M0 (the instruction's LDS base) is saved
+// and restored around the load.
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_addr, int voff) {
+    int save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(lds_addr), "v"(voff), "s"(rsrc)
+        : "memory");
+}
+
+// Buffer resources of one 64-position tile's rows of one kv head in the K and
+// V pools.  A resource starts at the tile's first row and ends after its row
+// at kv_hi, so rows past kv_hi (a page's unwritten tail may hold any bytes),
+// tiles of an invalid page and tiles past the block's range read as zeros.
+struct TileSrc {
+    __amdgpu_buffer_rsrc_t k, v;
+    bool ok;  // a valid page (wave-uniform)
+};
+
 template <int HD, int G>
 __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
-    constexpr int KC = HD / 16;
-    constexpr int DB = HD / 32;
-    constexpr int ROW = HD * 2 + 64;      // padded LDS row (bytes)
-    constexpr int CPR = HD / 8;           // 16-byte chunks per row
-    constexpr int CHUNKS = kPBN * CPR;    // 16-byte chunks per tile
-    constexpr int LPT = CHUNKS / 256;     // chunks per thread per tile
-    static_assert(CHUNKS % 256 == 0, "tile chunks");
+    constexpr int KC = HD / 16;          // 16-dim K operand steps per row
+    constexpr int DB = HD / 32;          // 32-dim output blocks
+    constexpr int RB = HD * 2;           // f16 row bytes
+    constexpr int CPR = RB / 16;         // 16-byte chunks per row
+    constexpr int TB = kPBN * RB;        // tile bytes (K or V)
+    constexpr int IPW = TB / 4096;       // 1 KB DMA instructions per wave per tile and tensor
+    constexpr int RPI = 1024 / RB;       // rows per 1 KB block
+    constexpr int NG = RB / 64;          // 64-byte groups per row
+    constexpr int RP = 256 / RB > 0 ? 256 / RB : 1;  // rows per 256 bytes (all LDS banks)
+    static_assert(TB % 4096 == 0 && 1024 % RB == 0, "tile split over four waves");
 
-    // double-buffered K and V tiles.  K rows are unpadded with the 16-byte
-    // chunk c of row r stored at chunk c ^ (r % CPR), so the 16 rows one
-    // 16-lane slice of an MFMA operand read touches cover all 64 LDS banks.
-    // V rows are padded by 64 bytes: a transposed read's 32-lane half reads
-    // 64 bytes from each of four consecutive rows, which then start 16 banks
-    // apart (no bank conflicts).
-    constexpr int KROW = HD * 2;
-    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * KROW];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kPBN * ROW];
+    // Two K and two V tiles, filled straight from the page.  K's 16-byte chunk
+    // c of row r sits at chunk c ^ (r % CPR): the 16 rows one 16-lane slice
+    // of an MFMA operand read touches cover all 64 LDS banks.  V's 64-byte
+    // group j of row r sits at group j ^ ((r / RP) % NG): the four rows a
+    // 32-lane half of a transposed read covers (64 bytes each) fall in
+    // disjoint banks.
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][TB];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][TB];
 
     // 1-D grid: workgroup L serves kv head L % Hkv and query block
     // n_qblk - 1 - L / Hkv (heaviest blocks first).  Workgroups go to the
@@ -162,183 +203,245 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     const int kvh = (int)blockIdx.x % p.n_head_kv;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 31;
     const int hh = lane >> 5;
-    const int Hkv = p.n_head_kv;
-    const int64_t col_bytes = (int64_t)Hkv * HD * 2;
+    const int col_bytes = p.n_head_kv * RB;
 
     // this lane's query row (MFMA column n): head g of the group, token tq
     const PrefillRows rows = prefill_rows<G>(p, wave, n);
     const bool row_ok = rows.row_ok;
     const int tq = rows.tq, h = rows.h;
-    const int kv_hi = rows.kv_hi, lo = rows.lo, tile0 = rows.tile0, tile1 = rows.tile1;
+    const int kv_hi = rows.kv_hi, tile0 = rows.tile0, tile1 = rows.tile1;
 
-    // cooperative tile loads into registers: chunk i*256 + tid -> row r =
-    // 16i + tid / CPR, 16-byte chunk c = tid % CPR.  Buffer loads: the tile's
-    // page base is a scalar resource (records end at the tile, so nothing past
-    // it is read), the lane offset a constant, row block i a scalar offset.
-    static_assert(256 % CPR == 0, "row blocks");
-    constexpr int RPI = 256 / CPR;  // rows per load instruction
-    half8 kreg[LPT], vreg[LPT];
-    bool page_ok = false;
-    const int lane_off = (tid / CPR) * (int)col_bytes + 16 * (tid % CPR);
-    auto load = [&](int t) {
-        const int pos0 = t * kPBN;
-        const int lp = pos0 / p.page_size;
-        const int32_t pid = __builtin_amdgcn_readfirstlane(lp < p.max_pages ? p.page_table[lp] : -1);
-        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
-        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
-        page_ok = kb != nullptr && vb != nullptr;
-        if (!page_ok) return;
-        const int64_t base = (int64_t)(pos0 - lp * p.page_size) * col_bytes + (int64_t)kvh * HD * 2;
-        const int n_rec = (int)(kPBN * col_bytes);
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(kb + base), 0, n_rec, kBufferRsrcWord3);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(vb + base), 0, n_rec, kBufferRsrcWord3);
+    // DMA lane offsets: block i of this wave holds rows (IPW wave + i) RPI +
+    // lane / CPR; the lane fills LDS chunk lane % CPR of its row, which holds
+    // the row's chunk (lane % CPR) ^ swizzle.
+    int k_off[IPW], v_off[IPW];
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int soff = i * RPI * (int)col_bytes;
-            kreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off, soff, 0));
-            vreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, lane_off, soff, 0));
-        }
-    };
-    // registers -> LDS buffer; V rows outside [lo, kv_hi] zeroed (a page's
-    // unwritten tail may hold any bytes), K rows are masked in the scores.
-    // Tiles wholly inside the range with a valid page store unmasked.
-    auto store = [&](int t, int buf) {
-        const int pos0 = t * kPBN;
-        const bool whole = page_ok && pos0 >= lo && pos0 + kPBN - 1 <= kv_hi;  // wave-uniform
-        if (whole) {
-#pragma unroll
-            for (int i = 0; i < LPT; ++i) {
-                const int id = i * 256 + tid;
-                const int r = id / CPR, c = id % CPR;
-                *reinterpret_cast<half8 *>(&lds_k[buf][r * KROW + 16 * (c ^ (r % CPR))]) = kreg[i];
-                *reinterpret_cast<half8 *>(&lds_v[buf][r * ROW + 16 * c]) = vreg[i];
-            }
-            return;
-        }
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int id = i * 256 + tid;
-            const int r = id / CPR, c = id % CPR;
-            const bool ok = page_ok && pos0 + r >= lo && pos0 + r <= kv_hi;
-            *reinterpret_cast<half8 *>(&lds_k[buf][r * KROW + 16 * (c ^ (r % CPR))]) = page_ok ? kreg[i] : half8{};
-            *reinterpret_cast<half8 *>(&lds_v[buf][r * ROW + 16 * c]) = ok ? vreg[i] : half8{};
-        }
-    };
+    for (int i = 0; i < IPW; ++i) {
+        const int r = (IPW * wave + i) * RPI + lane / CPR, cp = lane % CPR;
+        k_off[i] = r * col_bytes + 16 * (cp ^ (r % CPR));
+        v_off[i] = r * col_bytes + 16 * (cp ^ (4 * ((r / RP) % NG)));
+    }
+    const uint32_t lds_k0 = lds_u32(lds_k[0]) + 1024u * IPW * wave;
+    const uint32_t lds_v0 = lds_u32(lds_v[0]) + 1024u * IPW * wave;
 
-    load(tile0);
-
-    // Q^T operand of this lane's row, rounded to f16; every chunk is loaded
-    // before any is converted (rows past T read row 0 and are zeroed), so
-    // the prologue waits on memory once
-    half8 qf[KC];
+    // Page ids of 64 logical pages from the block's first one, one per lane:
+    // a tile's id is a v_readlane instead of a dependent scalar load ahead of
+    // every tile's loads.  The window moves (one reload) only when the block's
+    // kv range spans more than 64 pages.
+    PageWindow win;
+    win.load(p.page_table, p.max_pages, tile0 * kPBN / p.page_size, lane);
+    // Q of this lane's row (rows past T read row 0, zeroed below): its loads
+    // go out right after the page-id window's, so they overlap the wait for
+    // the window that the first tiles' loads need
+    floatx4 qx[KC][2];
     {
         const float *qr = p.q + ((int64_t)(row_ok ? tq : 0) * p.n_head + h) * HD;
-        floatx4 qx[KC][2];
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
             const floatx4 *src = reinterpret_cast<const floatx4 *>(qr + 16 * c + 8 * hh);
             qx[c][0] = src[0];
             qx[c][1] = src[1];
         }
+    }
+    // (logical page, first row in it) of tile t, advanced one tile per call
+    // (page_size is a multiple of the tile) instead of a division per tile
+    struct TilePos {
+        int lp, row;
+    };
+    auto advance = [&](TilePos &tp) {
+        tp.row += kPBN;
+        const bool wrap = tp.row == p.page_size;
+        tp.lp += wrap ? 1 : 0;
+        tp.row = wrap ? 0 : tp.row;
+    };
+    auto tile_src = [&](const TilePos &tp, int t) -> TileSrc {
+        const int32_t pid = tp.lp < p.max_pages ? win.get(p.page_table, p.max_pages, tp.lp, lane) : -1;
+        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        const int pos0 = t * kPBN;
+        const int r_hi = kv_hi - pos0 < kPBN - 1 ? kv_hi - pos0 : kPBN - 1;
+        TileSrc ts;
+        ts.ok = kb != nullptr && vb != nullptr;
+        const int n_rec = ts.ok && r_hi >= 0 ? r_hi * col_bytes + RB : 0;
+        const int64_t off = (int64_t)tp.row * col_bytes + (int64_t)kvh * RB;
+        ts.k = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ts.ok ? kb + off : p.k_pages), 0, n_rec,
+                                                 kBufferRsrcWord3);
+        ts.v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ts.ok ? vb + off : p.v_pages), 0, n_rec,
+                                                 kBufferRsrcWord3);
+        return ts;
+    };
+
+    // prologue: K and V of the first tile, K of the second (one tile ahead)
+    TilePos pos1{tile0 * kPBN / p.page_size, tile0 * kPBN % p.page_size};
+    const TileSrc src0 = tile_src(pos1, tile0);
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            half8 hv;
+    for (int i = 0; i < IPW; ++i) {
+        dma16(src0.k, lds_k0 + 1024u * i, k_off[i]);
+        dma16(src0.v, lds_v0 + 1024u * i, v_off[i]);
+    }
+    advance(pos1);
+    TileSrc src1 = tile_src(pos1, tile0 + 1);  // zeros past tile1
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hv[e] = (_Float16)qx[c][0][e];
-                hv[4 + e] = (_Float16)qx[c][1][e];
-            }
-            qf[c] = row_ok ? hv : half8{};
+    for (int i = 0; i < IPW; ++i) dma16(src1.k, lds_k0 + (uint32_t)TB + 1024u * i, k_off[i]);
+    bool dead_cur = !src0.ok;
+    TilePos pos2 = pos1;
+
+    // Q^T operand of this lane's row, rounded to f16
+    half8 qf[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        half8 hv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            hv[e] = (_Float16)qx[c][0][e];
+            hv[4 + e] = (_Float16)qx[c][1][e];
         }
+        qf[c] = row_ok ? hv : half8{};
     }
 
-    store(tile0, 0);
-    __syncthreads();
-
-    floatx16 o[DB];
-#pragma unroll
-    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
-    float m_run = -INFINITY, l_run = 0.0f;
-    const int gq = lane >> 4, rr = lane & 15;
-    const int tr_off = (4 * (gq >> 1) + (rr >> 2)) * ROW + 2 * (16 * (gq & 1) + 4 * (rr & 3));
-
-    for (int t = tile0; t <= tile1; ++t) {
-        const int buf = (t - tile0) & 1;
-        const int pos0 = t * kPBN;
-        if (t < tile1) load(t + 1);  // in flight while this tile computes
-        const uint8_t *kt = lds_k[buf];
-        const uint8_t *vt = lds_v[buf];
-
-        // S^T = K * Q^T for the two 32-position blocks, interleaved chains
-        floatx16 s[2] = {floatx16{}, floatx16{}};
+    // S^T = K * Q^T of the tile in K buffer kb (two 32-position blocks)
+    auto qk = [&](const uint8_t *kt, floatx16 (&s)[2]) {
+        s[0] = floatx16{};
+        s[1] = floatx16{};
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
 #pragma unroll
             for (int pb = 0; pb < 2; ++pb) {
                 const int r = 32 * pb + n;
-                const half8 a = *reinterpret_cast<const half8 *>(kt + r * KROW + 16 * ((2 * c + hh) ^ (r % CPR)));
+                const half8 a = *reinterpret_cast<const half8 *>(kt + r * RB + 16 * ((2 * c + hh) ^ (r % CPR)));
                 s[pb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s[pb], 0, 0, 0);
             }
         }
-        // masking only where the tile meets the window start, the diagonal
-        // or rows past T (wave-uniform branch); raw scores, the scale (> 0)
-        // is applied inside the exponent
-        if (prefill_edge(rows, pos0, false)) prefill_mask(s, rows, pos0, hh, false);
-        const float alpha = prefill_rescale(s, p.scale_log2, m_run);
-        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        half8 pbv[2][2];
+    };
+
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    floatx16 s[2];
+    qk(lds_k[0], s);
+    float m_run = -INFINITY, l_run = 0.0f;
+    if (prefill_edge(rows, tile0 * kPBN, dead_cur)) prefill_mask(s, rows, tile0 * kPBN, hh, dead_cur);
+    float alpha = prefill_rescale(s, p.scale_log2, m_run);
+
+    floatx16 o[DB];
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
+    for (int d = 0; d < DB; ++d) o[d] = floatx16{};
+
+    // V^T operand reads: lane rr of 16-lane group gq takes row 4(gq/2) + rr/4
+    // (+ the step's row offset, a multiple of 8), logical bytes 64d +
+    // 32(gq%2) + 8(rr%4), its 64-byte group swizzled by the row
+    const int gq = lane >> 4, rr = lane & 15;
+    int tr_off[DB];
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                pbv[pb][i >> 3][i & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[pb][i], p.scale_log2, -m_use));
-        }
-        // the row sum of the f16 weights the P*V product uses, two per
-        // v_dot2_f32_f16 into an f32 accumulator
-        float ls = 0.0f;
-        const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(HalfPairs, pbv[pb][kk]).v[j], ones, ls, false);
-        l_run = l_run * alpha + ls;
+    for (int d = 0; d < DB; ++d) {
+        const int r = 4 * (gq >> 1) + (rr >> 2);
+        tr_off[d] = r * RB + 64 * (d ^ ((r / RP) % NG)) + 32 * (gq & 1) + 8 * (rr & 3);
+    }
+    const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    // Tile t: K(t+1) and V(t) are in LDS once the barrier at the top has
+    // passed; K(t+2) and V(t+1) go into the buffers the previous trip
+    // finished with, one load instruction per QK region (issued together,
+    // every wave's loads would queue behind each other at the top of the
+    // trip), so each has most of a trip to land.  The trip computes P(t)
+    // from S(t) while the MFMAs form S(t+1), then O += V(t)^T P(t)^T.
+    for (int t = tile0; t <= tile1; ++t) {
+        const int j = t - tile0;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        advance(pos2);
+        const TileSrc src2 = tile_src(pos2, t + 2);  // zeros past tile1
+        const uint32_t k_dst = lds_k0 + (uint32_t)((j & 1) * TB);
+        const uint32_t v_dst = lds_v0 + (uint32_t)(((j + 1) & 1) * TB);
+        const bool dead_next = !src1.ok;
+
+        l_run *= alpha;
         if (__any(alpha != 1.0f)) {
 #pragma unroll
             for (int d = 0; d < DB; ++d) o[d] *= alpha;
         }
 
-        // O^T += V^T * P^T, V^T operands by transposed LDS reads
+        // P(t) = exp2(S(t) scale - m) (f16) beside S(t+1) = K(t+1) Q^T, then
+        // O^T += V(t)^T P(t)^T beside P's row sum, in short regions the
+        // scheduler may not reorder across (sched_barrier), so the MFMA pipe
+        // works on one while the VALU computes the other, and each region's
+        // LDS reads feed the next region's products.  (On the last tile the
+        // QK products read a stale buffer and are discarded.)
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        const uint8_t *kt = lds_k[(j + 1) & 1];
+        const uint8_t *vt = lds_v[j & 1];
+        auto k_read = [&](int c, half8 (&a)[2]) {
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                half8 va[DB];
-#pragma unroll
-                for (int d = 0; d < DB; ++d) {
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const half4 hv = tr16_read(vt + tr_off + (32 * pb + 16 * kk + 8 * u) * ROW + 64 * d);
-                        va[d][4 * u + 0] = hv[0];
-                        va[d][4 * u + 1] = hv[1];
-                        va[d][4 * u + 2] = hv[2];
-                        va[d][4 * u + 3] = hv[3];
-                    }
-                }
-#pragma unroll
-                for (int d = 0; d < DB; ++d)
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d], pbv[pb][kk], o[d], 0, 0, 0);
+            for (int pb = 0; pb < 2; ++pb) {
+                const int r = 32 * pb + n;
+                a[pb] = *reinterpret_cast<const half8 *>(kt + r * RB + 16 * ((2 * c + hh) ^ (r % CPR)));
             }
+        };
+        auto v_read = [&](int step, half8 (&va)[DB]) {  // step = 2 pb + kk
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const half4 hv = tr16_read(vt + tr_off[d] + (16 * step + 8 * u) * RB);
+                    va[d][4 * u + 0] = hv[0];
+                    va[d][4 * u + 1] = hv[1];
+                    va[d][4 * u + 2] = hv[2];
+                    va[d][4 * u + 3] = hv[3];
+                }
+            }
+        };
+        constexpr int EPC = 32 / KC;  // exponentials per QK chunk
+        half8 pbv[2][2];
+        floatx16 sn[2] = {floatx16{}, floatx16{}};
+        half8 ka[2], kb[2], va[DB], vb[DB];
+        k_read(0, ka);
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            if (c + 1 < KC) k_read(c + 1, kb);
+            if (c + 1 == KC) v_read(0, va);
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb) sn[pb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[pb], qf[c], sn[pb], 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+                const int i = EPC * c + e;  // score i % 16 of block i / 16
+                pbv[i >> 4][(i >> 3) & 1][i & 7] =
+                    (_Float16)__builtin_amdgcn_exp2f(fmaf(s[i >> 4][i & 15], p.scale_log2, -m_use));
+            }
+            if (c < IPW) dma16(src2.k, k_dst + 1024u * c, k_off[c]);
+            else if (c < 2 * IPW) dma16(src1.v, v_dst + 1024u * (c - IPW), v_off[c - IPW]);
+            __builtin_amdgcn_sched_barrier(0);
+            ka[0] = kb[0];
+            ka[1] = kb[1];
         }
-        if (t < tile1) store(t + 1, buf ^ 1);
-        __syncthreads();
+        float ls = 0.0f;
+#pragma unroll
+        for (int step = 0; step < 4; ++step) {
+            if (step + 1 < 4) v_read(step + 1, vb);
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d], pbv[step >> 1][step & 1], o[d], 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(HalfPairs, pbv[step >> 1][step & 1]).v[e], ones,
+                                            ls, false);
+            asm volatile("" : "+v"(ls));  // keeps the sums in this region
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) va[d] = vb[d];
+        }
+        l_run += ls;
+
+        // masking of S(t+1) only where it meets the window start, the
+        // diagonal or rows past T, or for an invalid page (wave-uniform)
+        if (t < tile1 && prefill_edge(rows, (t + 1) * kPBN, dead_next))
+            prefill_mask(sn, rows, (t + 1) * kPBN, hh, dead_next);
+        alpha = prefill_rescale(sn, p.scale_log2, m_run);
+        s[0] = sn[0];
+        s[1] = sn[1];
+        src1 = src2;
     }
 
     prefill_write<HD>(o, l_run, rows, p, hh);
