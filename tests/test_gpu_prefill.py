@@ -254,3 +254,23 @@ def test_prefill_late_rescale(gpu, oracle_mod, kv_type):
         assert_close(out, ref, max_abs=F32_MAX_ABS, rel_l2=F32_REL, what="f32 late rescale vs ggml")
     else:
         assert_close(out, ref, what=f"type {kv_type} late rescale vs ggml")
+
+
+@pytest.mark.parametrize("kv_type", [0, 1, 8])
+@pytest.mark.parametrize("bad", ["missing", "out_of_pool"])
+def test_prefill_invalid_first_page(gpu, oracle_mod, kv_type, bad):
+    # the history's first page has no valid id (-1, or an id past the pool):
+    # its tiles arrive as zeros, are masked and contribute nothing, so every
+    # row equals attention over the positions from the second page on (the
+    # same call with kv_lo at that page's first position); nothing is read out
+    # of bounds
+    ps, n_cached, T = 256, 600, 100
+    host, dev, pt, q, n_kv = build(oracle_mod, gpu, Hq=32, Hkv=8, hd=128, n_cached=n_cached, T=T,
+                                   page_size=ps, seed=31 + kv_type, kv_type=kv_type)
+    bad_pt = pt.copy()
+    bad_pt[0, 0] = -1 if bad == "missing" else dev.n_pages + 100
+    out = run(dev, gpu, bad_pt, q, n_cached)
+    ref = host.attention(q[None], 32, pt, np.array([n_kv], np.int32), np.array([ps], np.int32),
+                         T=T, mode=oracle_mod.GGML)[0].reshape(T, -1)
+    assert np.all(np.isfinite(out))
+    assert_close(out, ref, what=f"type {kv_type}, {bad} first page")
