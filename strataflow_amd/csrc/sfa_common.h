@@ -103,6 +103,30 @@ __device__ inline float xor32(float x) {
     return __shfl_xor(x, 32, 64);
 }
 
+// Both halves of x in every lane, by one v_permlane32_swap (a VALU op, no
+// LDS round trip): lo = x of lane l % 32, hi = x of lane 32 + l % 32.  The
+// builtin's pair is read by bytes: indexing its second element returned the
+// first one with this compiler.
+__device__ inline void swap_halves(float x, float &lo, float &hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
+                                                    false, false);
+    static_assert(sizeof(r) == 8, "two 32-bit lanes values");
+    unsigned u0, u1;
+    __builtin_memcpy(&u0, reinterpret_cast<const char *>(&r), 4);
+    __builtin_memcpy(&u1, reinterpret_cast<const char *>(&r) + 4, 4);
+    lo = __builtin_bit_cast(float, u0);
+    hi = __builtin_bit_cast(float, u1);
+}
+
+// max(a, b, c) in one v_max3_f32.  fmaxf makes the compiler quiet signalling
+// NaNs first (one more v_max per operand); for MFMA results and -INF masks
+// that cannot occur, and the result is the same.
+__device__ inline float max3_raw(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // Value of another lane of the same 16-lane row, DPP control CTRL (all rows
 // and banks enabled, every source lane inside the row).
 template <int CTRL>

@@ -41,6 +41,10 @@ struct PrefillParams {
 
 constexpr int kPBN = 64;           // positions per prefill tile
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale threshold (P <= 2^8)
+template <int N>
+struct IntC {  // a compile-time int passed to a generic lambda
+    static constexpr int value = N;
+};
 struct HalfPairs {
     half2v v[4];  // the four dwords of a half8
 };
@@ -104,16 +108,22 @@ __device__ __attribute__((always_inline)) inline void prefill_mask(floatx16 (&s)
 // it by 2^8 (P stays <= 256; exact since O and l share the reference).
 // Returns the factor O and l are rescaled by (1 when the reference stays).
 __device__ __attribute__((always_inline)) inline float prefill_rescale(const floatx16 (&s)[2], float scale_log2, float &m_run) {
-    // a reduction tree (5 levels) rather than a 32-long dependent chain
-    float a[16];
+    // a v_max3 tree (4 levels, 16 instructions) rather than a 32-long chain
+    float a[11], b[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) a[i] = fmaxf(s[0][i], s[1][i]);
+    for (int i = 0; i < 10; ++i) {
+        const int k = 3 * i;
+        a[i] = max3_raw(s[k >> 4][k & 15], s[(k + 1) >> 4][(k + 1) & 15], s[(k + 2) >> 4][(k + 2) & 15]);
+    }
+    a[10] = max3_raw(s[1][14], s[1][15], s[1][15]);
 #pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-        for (int i = 0; i < w; ++i) a[i] = fmaxf(a[i], a[i + w]);
-    float mt = a[0];
-    mt = fmaxf(mt, xor32(mt)) * scale_log2;
+    for (int i = 0; i < 3; ++i) b[i] = max3_raw(a[3 * i], a[3 * i + 1], a[3 * i + 2]);
+    b[3] = max3_raw(a[9], a[10], a[10]);
+    const float lane_max = max3_raw(max3_raw(b[0], b[1], b[2]), b[3], b[3]);
+    // the other half of the row: lanes l and l ^ 32 hold the same query row
+    float lo, hi;
+    swap_halves(lane_max, lo, hi);
+    const float mt = max3_raw(lo, hi, hi) * scale_log2;
     float alpha = 1.0f;
     if (mt > m_run + kRescaleLog2) {
         alpha = __builtin_amdgcn_exp2f(m_run - mt);  // m_run == -inf -> 0
@@ -347,15 +357,17 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
     // finished with, one load instruction per QK region (issued together,
     // every wave's loads would queue behind each other at the top of the
     // trip), so each has most of a trip to land.  The trip computes P(t)
-    // from S(t) while the MFMAs form S(t+1), then O += V(t)^T P(t)^T.
-    for (int t = tile0; t <= tile1; ++t) {
-        const int j = t - tile0;
+    // from S(t) while the MFMAs form S(t+1), then O += V(t)^T P(t)^T.  Trips
+    // come in pairs (PAR = (t - tile0) % 2) so that the buffers are fixed per
+    // trip and S(t) and S(t+1) swap register sets instead of being copied.
+    auto trip = [&](int t, auto par, floatx16(&s)[2], floatx16(&sn)[2]) {
+        constexpr int PAR = decltype(par)::value;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         advance(pos2);
         const TileSrc src2 = tile_src(pos2, t + 2);  // zeros past tile1
-        const uint32_t k_dst = lds_k0 + (uint32_t)((j & 1) * TB);
-        const uint32_t v_dst = lds_v0 + (uint32_t)(((j + 1) & 1) * TB);
+        const uint32_t k_dst = lds_k0 + (uint32_t)(PAR * TB);
+        const uint32_t v_dst = lds_v0 + (uint32_t)((1 - PAR) * TB);
         const bool dead_next = !src1.ok;
 
         l_run *= alpha;
@@ -371,16 +383,16 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         // LDS reads feed the next region's products.  (On the last tile the
         // QK products read a stale buffer and are discarded.)
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        const uint8_t *kt = lds_k[(j + 1) & 1];
-        const uint8_t *vt = lds_v[j & 1];
-        auto k_read = [&](int c, half8 (&a)[2]) {
+        const uint8_t *kt = lds_k[1 - PAR];
+        const uint8_t *vt = lds_v[PAR];
+        auto k_read = [&](int c, half8(&a)[2]) {
 #pragma unroll
             for (int pb = 0; pb < 2; ++pb) {
                 const int r = 32 * pb + n;
                 a[pb] = *reinterpret_cast<const half8 *>(kt + r * RB + 16 * ((2 * c + hh) ^ (r % CPR)));
             }
         };
-        auto v_read = [&](int step, half8 (&va)[DB]) {  // step = 2 pb + kk
+        auto v_read = [&](int step, half8(&va)[DB]) {  // step = 2 pb + kk
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -395,7 +407,8 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         };
         constexpr int EPC = 32 / KC;  // exponentials per QK chunk
         half8 pbv[2][2];
-        floatx16 sn[2] = {floatx16{}, floatx16{}};
+        sn[0] = floatx16{};
+        sn[1] = floatx16{};
         half8 ka[2], kb[2], va[DB], vb[DB];
         k_read(0, ka);
 #pragma unroll
@@ -439,9 +452,14 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         if (t < tile1 && prefill_edge(rows, (t + 1) * kPBN, dead_next))
             prefill_mask(sn, rows, (t + 1) * kPBN, hh, dead_next);
         alpha = prefill_rescale(sn, p.scale_log2, m_run);
-        s[0] = sn[0];
-        s[1] = sn[1];
         src1 = src2;
+    };
+    floatx16 s1[2];
+    for (int t = tile0;; t += 2) {
+        trip(t, IntC<0>{}, s, s1);
+        if (t + 1 > tile1) break;
+        trip(t + 1, IntC<1>{}, s1, s);
+        if (t + 2 > tile1) break;
     }
 
     prefill_write<HD>(o, l_run, rows, p, hh);
