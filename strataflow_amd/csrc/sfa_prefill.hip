@@ -159,20 +159,21 @@ __device__ inline uint32_t lds_u32(const void *ptr) {
 // (past num_records a lane reads zeros).  Issued from asm, so the compiler
 // does not count these loads: its own LDS reads of the other buffers do not
 // wait for them, and the caller waits with s_waitcnt vmcnt before the
-// barrier that publishes the tile.  M0 (the instruction's LDS base) is saved
-// and restored around the load.
+// barrier that publishes the tile.  M0 holds the instruction's LDS base; it
+// is declared clobbered (the kernels that call this use M0 for nothing else,
+// and the compiler sets M0 itself before any use of its own).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // "m0 is reserved": intended, as above
 __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_addr, int voff) {
-    int save;
     asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
+        "s_mov_b32 m0, %0\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(save)
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
         : "s"(lds_addr), "v"(voff), "s"(rsrc)
-        : "memory");
+        : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Buffer resources of one 64-position tile's rows of one kv head in the K and
 // V pools.  A resource starts at the tile's first row and ends after its row
@@ -267,33 +268,46 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         tp.lp += wrap ? 1 : 0;
         tp.row = wrap ? 0 : tp.row;
     };
-    auto tile_src = [&](const TilePos &tp, int t) -> TileSrc {
-        const int32_t pid = tp.lp < p.max_pages ? win.get(p.page_table, p.max_pages, tp.lp, lane) : -1;
-        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
-        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+    // the K and V pages of logical page lp (nullptr both for an invalid id),
+    // resolved once per page rather than once per tile (the scalar unit is
+    // shared by the CU's eight waves)
+    struct PageSrc {
+        const uint8_t *kb, *vb;
+    };
+    auto page_src = [&](int lp) -> PageSrc {
+        const int32_t pid = lp < p.max_pages ? win.get(p.page_table, p.max_pages, lp, lane) : -1;
+        PageSrc ps;
+        ps.kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+        ps.vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        if (ps.kb == nullptr || ps.vb == nullptr) ps.kb = ps.vb = nullptr;
+        return ps;
+    };
+    auto tile_src = [&](const PageSrc &ps, const TilePos &tp, int t) -> TileSrc {
         const int pos0 = t * kPBN;
         const int r_hi = kv_hi - pos0 < kPBN - 1 ? kv_hi - pos0 : kPBN - 1;
         TileSrc ts;
-        ts.ok = kb != nullptr && vb != nullptr;
+        ts.ok = ps.kb != nullptr;
         const int n_rec = ts.ok && r_hi >= 0 ? r_hi * col_bytes + RB : 0;
         const int64_t off = (int64_t)tp.row * col_bytes + (int64_t)kvh * RB;
-        ts.k = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ts.ok ? kb + off : p.k_pages), 0, n_rec,
+        ts.k = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ts.ok ? ps.kb + off : p.k_pages), 0, n_rec,
                                                  kBufferRsrcWord3);
-        ts.v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ts.ok ? vb + off : p.v_pages), 0, n_rec,
+        ts.v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ts.ok ? ps.vb + off : p.v_pages), 0, n_rec,
                                                  kBufferRsrcWord3);
         return ts;
     };
 
     // prologue: K and V of the first tile, K of the second (one tile ahead)
     TilePos pos1{tile0 * kPBN / p.page_size, tile0 * kPBN % p.page_size};
-    const TileSrc src0 = tile_src(pos1, tile0);
+    PageSrc page2 = page_src(pos1.lp);
+    const TileSrc src0 = tile_src(page2, pos1, tile0);
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
         dma16(src0.k, lds_k0 + 1024u * i, k_off[i]);
         dma16(src0.v, lds_v0 + 1024u * i, v_off[i]);
     }
     advance(pos1);
-    TileSrc src1 = tile_src(pos1, tile0 + 1);  // zeros past tile1
+    if (pos1.row == 0) page2 = page_src(pos1.lp);
+    TileSrc src1 = tile_src(page2, pos1, tile0 + 1);  // zeros past tile1
 #pragma unroll
     for (int i = 0; i < IPW; ++i) dma16(src1.k, lds_k0 + (uint32_t)TB + 1024u * i, k_off[i]);
     bool dead_cur = !src0.ok;
@@ -365,7 +379,8 @@ __global__ __launch_bounds__(256, 2) void prefill_f16_kernel(PrefillParams p) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         advance(pos2);
-        const TileSrc src2 = tile_src(pos2, t + 2);  // zeros past tile1
+        if (pos2.row == 0) page2 = page_src(pos2.lp);
+        const TileSrc src2 = tile_src(page2, pos2, t + 2);  // zeros past tile1
         const uint32_t k_dst = lds_k0 + (uint32_t)(PAR * TB);
         const uint32_t v_dst = lds_v0 + (uint32_t)((1 - PAR) * TB);
         const bool dead_next = !src1.ok;
