@@ -649,7 +649,7 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
     constexpr int SW = QROW / 16 - 1;     // K chunk swizzle mask
     constexpr int RB = NB * kQ8Bytes;     // bytes of one cache row
     __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * QROW];
-    __shared__ __attribute__((aligned(16))) _Float16 lds_dk[2][NB][kPBN];
+    __shared__ __attribute__((aligned(16))) float lds_dk[2][NB][kPBN];  // d_k as f32 (converted once, at staging)
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[2][kPBN * ROW];
 
     const int kvh = (int)blockIdx.x % p.n_head_kv;
@@ -671,12 +671,22 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
     const int sp_ = tid / NB, sc = tid % NB;
     uint32_t kraw[9], vraw[9];
     bool page_ok = false;
+    // page ids of 64 logical pages, one per lane (a tile's id is a
+    // v_readlane, not a dependent load ahead of its data loads), and the
+    // current page's K and V bases, resolved once per page
+    PageWindow win;
+    win.load(p.page_table, p.max_pages, tile0 * kPBN / p.page_size, lane);
+    int cur_lp = -1;
+    const uint8_t *kb = nullptr, *vb = nullptr;
     auto load = [&](int t) {
         const int pos0 = t * kPBN;
         const int lp = pos0 / p.page_size;
-        const int32_t pid = __builtin_amdgcn_readfirstlane(lp < p.max_pages ? p.page_table[lp] : -1);
-        const uint8_t *kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
-        const uint8_t *vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        if (lp != cur_lp) {
+            cur_lp = lp;
+            const int32_t pid = lp < p.max_pages ? win.get(p.page_table, p.max_pages, lp, lane) : -1;
+            kb = page_base(pid, p.k_pages, p.n_pages, p.k_cold, p.n_cold, p.page_bytes);
+            vb = page_base(pid, p.v_pages, p.n_pages, p.v_cold, p.n_cold, p.page_bytes);
+        }
         page_ok = kb != nullptr && vb != nullptr;
         if (!page_ok || !stager) return;
         // the 36 bytes at or 2 below the block (rows are 4-byte aligned)
@@ -726,7 +736,7 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
             intx4{(int)kq[0], (int)kq[1], (int)kq[2], (int)kq[3]};
         *reinterpret_cast<intx4 *>(krow + 16 * ((2 * sc + 1) ^ (sp_ & SW))) =
             intx4{(int)kq[4], (int)kq[5], (int)kq[6], (int)kq[7]};
-        lds_dk[buf][sc][sp_] = __builtin_bit_cast(_Float16, (uint16_t)kd);
+        lds_dk[buf][sc][sp_] = (float)__builtin_bit_cast(_Float16, (uint16_t)kd);
         // q * d rounded to f16 on packed halves, as in the Q8_0 decode kernel
         const bool ok = page_ok && pos0 + sp_ >= lo && pos0 + sp_ <= kv_hi;
         const _Float16 dv = ok ? __builtin_bit_cast(_Float16, (uint16_t)vd) : (_Float16)0.0f;
@@ -819,7 +829,7 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     // d_k of positions 32pb + 8j + 4hh + 0..3
-                    const half4 dk4 = *reinterpret_cast<const half4 *>(&lds_dk[buf][c][32 * pb + 8 * j + 4 * hh]);
+                    const floatx4 dk4 = *reinterpret_cast<const floatx4 *>(&lds_dk[buf][c][32 * pb + 8 * j + 4 * hh]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         s[pb][4 * j + e] += (float)acc[4 * j + e] * ((float)dk4[e] * dq[c]);
