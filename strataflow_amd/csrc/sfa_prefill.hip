@@ -637,8 +637,10 @@ __global__ __launch_bounds__(256, 1) void prefill_f32_kernel(PrefillParams p) {
 // (q * d rounded once) into the f16 kernel's V tile, and the softmax and P*V
 // are the f16 kernel's.  Tiles are staged through registers: one thread per
 // (position, block) loads the 34-byte block (and the V block) as 4-aligned
-// dwords, then writes the quants to a 16-byte-aligned K tile (chunks XOR-
-// swizzled by row), the scale to a per-block scale row, and the dequantised V.
+// dwords, then writes the quants to a 16-byte-aligned K tile (16-byte chunks
+// XOR-swizzled by row / (rows per 256 bytes), so the 16 rows of an operand read
+// and the 4 x 4 chunks of a staging write each cover all 64 LDS banks), the
+// scale to a per-block scale row (f32), and the dequantised V.
 template <int HD, int G>
 __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
     static_assert(HD == 64 || HD == 128, "head_dim");
@@ -647,6 +649,7 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
     constexpr int ROW = HD * 2 + 64;      // padded f16 V row (bytes)
     constexpr int QROW = HD;              // int8 K row in LDS (bytes)
     constexpr int SW = QROW / 16 - 1;     // K chunk swizzle mask
+    constexpr int RPB = 256 / QROW;       // K rows per 256 bytes (all 64 LDS banks)
     constexpr int RB = NB * kQ8Bytes;     // bytes of one cache row
     __shared__ __attribute__((aligned(16))) uint8_t lds_k[2][kPBN * QROW];
     __shared__ __attribute__((aligned(16))) float lds_dk[2][NB][kPBN];  // d_k as f32 (converted once, at staging)
@@ -732,9 +735,9 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
             for (int j = 0; j < 8; ++j) kq[j] = 0u;
         }
         uint8_t *krow = &lds_k[buf][sp_ * QROW];
-        *reinterpret_cast<intx4 *>(krow + 16 * ((2 * sc) ^ (sp_ & SW))) =
+        *reinterpret_cast<intx4 *>(krow + 16 * ((2 * sc) ^ ((sp_ / RPB) & SW))) =
             intx4{(int)kq[0], (int)kq[1], (int)kq[2], (int)kq[3]};
-        *reinterpret_cast<intx4 *>(krow + 16 * ((2 * sc + 1) ^ (sp_ & SW))) =
+        *reinterpret_cast<intx4 *>(krow + 16 * ((2 * sc + 1) ^ ((sp_ / RPB) & SW))) =
             intx4{(int)kq[4], (int)kq[5], (int)kq[6], (int)kq[7]};
         lds_dk[buf][sc][sp_] = (float)__builtin_bit_cast(_Float16, (uint16_t)kd);
         // q * d rounded to f16 on packed halves, as in the Q8_0 decode kernel
@@ -824,7 +827,7 @@ __global__ __launch_bounds__(256, 2) void prefill_q8_kernel(PrefillParams p) {
             const int r = 32 * pb + n;
 #pragma unroll
             for (int c = 0; c < NB; ++c) {
-                const intx4 a = *reinterpret_cast<const intx4 *>(kt + r * QROW + 16 * ((2 * c + hh) ^ (r & SW)));
+                const intx4 a = *reinterpret_cast<const intx4 *>(kt + r * QROW + 16 * ((2 * c + hh) ^ ((r / RPB) & SW)));
                 const intx16 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qa[c], intx16{}, 0, 0, 0);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
