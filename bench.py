@@ -413,10 +413,10 @@ def layer_bench(torch, steps: int, warmup: int, seed: int, n_layer: int = 8) -> 
     4096, 32 q / 8 kv heads of 128, 8 experts top-2, n_ff 14336; f16 weights
     N(0,1)*0.02, distinct per layer) over distinct f16 caches at context 4096,
     B = 1, one token per step through every layer, the step captured as one HIP
-    graph: rms_norm, the Q/K/V product (the three weights stacked), fused RoPE
-    + KV append, attention, the wo product with the residual added in the same
-    pass, rms_norm, the router
-    product, routing, the two routed experts' SwiGLU FFN and the residual.
+    graph: rms_norm, the Q/K/V product (the three weights stacked) with RoPE
+    and the KV append in the same launch, attention, the wo product with the residual added in the same
+    pass, rms_norm with the router product and the routing (one launch), the
+    two routed experts' SwiGLU FFN and the residual.
     The roofline counts the bytes a layer-token reads once: the Q/K/V, wo and
     router weights, the two routed experts' gate, up and down rows, the KV
     history (activations are a few KB)."""
@@ -446,28 +446,23 @@ def layer_bench(torch, steps: int, warmup: int, seed: int, n_layer: int = 8) -> 
                   torch.zeros(hist, device=dev, dtype=torch.int32), pos, pt)
     x0 = torch.randn((1, D), device=dev, generator=gen)
     x = torch.empty_like(x0)
-    cur, ffn_inp, qkv = torch.empty_like(x0), torch.empty_like(x0), torch.empty((1, (HQ + 2 * HKV) * HD), device=dev)
+    cur, ffn_inp = torch.empty_like(x0), torch.empty_like(x0)
+    q = torch.empty((1, HQ, HD), device=dev)
     ids, wts = torch.empty((1, K), dtype=torch.int32, device=dev), torch.empty((1, K), device=dev)
     moe_ws = torch.empty(K * F * 4, dtype=torch.uint8, device=dev)
     pos1 = torch.tensor([hist], dtype=torch.int32, device=dev)
     seq1 = torch.zeros(1, dtype=torch.int32, device=dev)
     sl = torch.tensor([ctx], dtype=torch.int32, device=dev)
-    q = qkv[:, :HQ * HD].view(1, HQ, HD)
-    k = qkv[:, HQ * HD:(HQ + HKV) * HD].view(1, HKV, HD)
-    v = qkv[:, (HQ + HKV) * HD:].view(1, HKV, HD)
-
     attn = torch.empty((1, HQ * HD), device=dev)
 
     def step():
         x.copy_(x0)
         for il, L in enumerate(layers):
             ops.rms_norm(x, L["attn_norm"], 1e-5, out=cur)
-            ops.mul_mat_vec(L["wqkv"], cur, out=qkv)
-            kv.rope_append(il, q, k, v, seq1, pos1, pt, 1e6)
+            kv.qkv_rope_append(il, L["wqkv"], cur, seq1, pos1, pt, 1e6, q=q)
             kv.decode(il, q, pt, sl, ctx, out=attn)
             ops.mul_mat_vec(L["wo"], attn, residual=x, out=ffn_inp)
-            ops.rms_norm(ffn_inp, L["ffn_norm"], 1e-5, out=cur)
-            ops.moe_gate(L["gate_inp"], cur, K, ids=ids, weights=wts)
+            ops.moe_norm_gate(ffn_inp, L["ffn_norm"], 1e-5, L["gate_inp"], K, out=cur, ids=ids, weights=wts)
             ops.moe_ffn(cur, ffn_inp, ids, wts, L["gate"], L["up"], L["down"], out=x, workspace=moe_ws)
 
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -9,12 +9,15 @@
  *   cur     = rms_norm(x) * attn_norm         sfa_rms_norm            engine.cpp:1879-1880
  *   Q, K, V = Wq/Wk/Wv * cur                  sfa_mul_mat_vec         engine.cpp:1883-1885
  *   RoPE, KV append, attention                sfa.h                   engine.cpp:1892-1901
+ *             (the product, RoPE and the
+ *              append in one launch:          sfa_qkv_rope_kv_append)
  *   ffn_inp = Wo * attn + x                   sfa_mul_mat_vec         engine.cpp:1905-1906
  *             (the residual added in the same pass)
  *   cur     = rms_norm(ffn_inp) * ffn_norm    sfa_rms_norm            engine.cpp:1908-1909
  *   logits  = gate_inp * cur                  sfa_mul_mat_vec         engine.cpp:1912
  *   ids, w  = top-k of softmax, renormalised  sfa_moe_route           engine.cpp:1913-1925
- *             (both in one launch:            sfa_moe_gate)
+ *             (both in one launch:            sfa_moe_gate;
+ *              with the ffn_norm too:         sfa_moe_norm_gate)
  *   x'      = sum_j w_j * down_j(silu(gate_j * cur) * (up_j * cur)) + ffn_inp
  *                                             sfa_moe_ffn             engine.cpp:1964-1984
  *
@@ -66,6 +69,34 @@ SFA_API int sfa_moe_route(const float *logits, int32_t n_rows, int32_t n_expert,
 SFA_API int sfa_moe_gate(const void *gate_inp, int32_t w_type, const float *x, int32_t n_rows,
                          int32_t n_embd, int32_t n_expert, int32_t n_used, int32_t *ids,
                          float *weights, void *stream);
+
+/* ffn_norm, the router product and the gating in one launch (engine.cpp:
+ * 1908-1925): y = rms_norm(x) * norm_weight (sfa_rms_norm's arithmetic; y is
+ * the experts' input), then sfa_moe_gate on y.  The results equal those two
+ * calls bit for bit, with one launch less.  x, y [n_rows][n_embd] f32,
+ * norm_weight [n_embd] f32, gate_inp [n_expert][n_embd] of w_type; n_embd a
+ * multiple of 8 and <= 8192, n_expert <= 64 (else SFA_ERR_UNSUPPORTED). */
+SFA_API int sfa_moe_norm_gate(const float *x, const float *norm_weight, float eps, const void *gate_inp,
+                              int32_t w_type, int32_t n_rows, int32_t n_embd, int32_t n_expert,
+                              int32_t n_used, float *y, int32_t *ids, float *weights, void *stream);
+
+/* The stacked Q/K/V product, RoPE NORMAL and the KV append in one launch
+ * (engine.cpp:1883-1885, 1892-1897, 1646-1656): the results of
+ * sfa_mul_mat_vec(w_qkv, x) followed by sfa_rope_kv_append on its Q, K and V
+ * parts, bit for bit, without the intermediate Q/K/V rows.
+ *   w_qkv : [(n_head + 2 n_head_kv) * head_dim][n_embd] of w_type (the Q, K
+ *           and V weights stacked row-wise), x : [n_tok][n_embd] f32
+ *   q     : out, [n_tok][n_head][head_dim] f32, rotated (as computed for a
+ *           token with seq or pos < 0, whose K/V are not written)
+ *   seq, pos, page_table, max_pages, freq_base : as sfa_rope_kv_append.
+ * F16 and F32 caches; SFA_ERR_UNSUPPORTED for Q8_0 (a block spans 16 RoPE
+ * pairs: use the two calls).  One workgroup reads the whole weight matrix per
+ * token, so this is the decode path; a long chunk is better served by
+ * sfa_mul_mat_vec + sfa_rope_kv_append. */
+SFA_API int sfa_qkv_rope_kv_append(const sfa_kv_desc *kv, const void *w_qkv, int32_t w_type,
+                                   const float *x, int32_t n_embd, float *q, const int32_t *seq,
+                                   const int32_t *pos, int32_t n_tok, const int32_t *page_table,
+                                   int32_t max_pages, float freq_base, void *stream);
 
 /* Workspace bytes of sfa_moe_ffn (the SwiGLU activations, n_rows * n_used *
  * n_ff floats); 0 for an invalid shape. */

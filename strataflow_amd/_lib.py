@@ -49,6 +49,8 @@ LAYER_EXPORTS = (
     "sfa_mul_mat_vec",
     "sfa_moe_route",
     "sfa_moe_gate",
+    "sfa_moe_norm_gate",
+    "sfa_qkv_rope_kv_append",
     "sfa_moe_workspace_bytes",
     "sfa_moe_ffn",
 )
@@ -135,6 +137,10 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_moe_route.restype = ctypes.c_int
     lib.sfa_moe_gate.argtypes = [P, i32, P, i32, i32, i32, i32, P, P, P]
     lib.sfa_moe_gate.restype = ctypes.c_int
+    lib.sfa_moe_norm_gate.argtypes = [P, P, ctypes.c_float, P, i32, i32, i32, i32, i32, P, P, P, P]
+    lib.sfa_moe_norm_gate.restype = ctypes.c_int
+    lib.sfa_qkv_rope_kv_append.argtypes = [D, P, i32, P, i32, P, P, P, i32, P, i32, ctypes.c_float, P]
+    lib.sfa_qkv_rope_kv_append.restype = ctypes.c_int
     lib.sfa_moe_workspace_bytes.argtypes = [i32, i32, i32]
     lib.sfa_moe_workspace_bytes.restype = ctypes.c_size_t
     lib.sfa_moe_ffn.argtypes = [P, P, P, P, P, P, P, i32, i32, i32, i32, i32, i32, P, ctypes.c_size_t, P, P]

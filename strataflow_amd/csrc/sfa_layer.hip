@@ -24,7 +24,7 @@
 // [n_in, n_out]); expert stacks are [n_expert][n_out][n_in].
 #include <exception>
 
-#include "sfa_common.h"
+#include "sfa_append.h"
 #include "sfa_layer.h"
 
 namespace sfa {
@@ -75,11 +75,10 @@ __device__ inline float dot8(const floatx4 w0, const floatx4 w1, const floatx4 x
 // the rest.
 constexpr int kNormThreads = 256;
 constexpr int kNormRegs = 16;
-__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *x, const float *w, float *y, int n,
-                                                                float eps) {
-    __shared__ double part[kNormThreads / 64];
-    const float *xr = x + (int64_t)blockIdx.x * n;
-    float *yr = y + (int64_t)blockIdx.x * n;
+// The norm of one row by a kNormThreads workgroup, written to yr and, when
+// ly is not null, to ly (an LDS copy for a consumer in the same workgroup).
+__device__ inline void norm_row(const float *xr, const float *w, float *yr, float *ly, int n, float eps,
+                                double *part) {
     const int tid = threadIdx.x;
     float xv[kNormRegs], wv[kNormRegs];
 #pragma unroll
@@ -109,10 +108,23 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *x, 
 #pragma unroll
     for (int k = 0; k < kNormRegs; ++k) {
         const int i = tid + kNormThreads * k;
-        if (i < n) yr[i] = __fmul_rn(__fmul_rn(xv[k], scale), wv[k]);
+        if (i < n) {
+            const float v = __fmul_rn(__fmul_rn(xv[k], scale), wv[k]);
+            yr[i] = v;
+            if (ly != nullptr) ly[i] = v;
+        }
     }
-    for (int i = tid + kNormThreads * kNormRegs; i < n; i += kNormThreads)
-        yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+    for (int i = tid + kNormThreads * kNormRegs; i < n; i += kNormThreads) {
+        const float v = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+        yr[i] = v;
+        if (ly != nullptr) ly[i] = v;
+    }
+}
+
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float *x, const float *w, float *y, int n,
+                                                                float eps) {
+    __shared__ double part[kNormThreads / 64];
+    norm_row(x + (int64_t)blockIdx.x * n, w, y + (int64_t)blockIdx.x * n, nullptr, n, eps, part);
 }
 
 // ---- mul_mat_vec ---------------------------------------------------------------
@@ -243,14 +255,11 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
 // one workgroup per token; wave w computes the logits of experts w, w + 4, ..
 // (the mul_mat_vec arithmetic), wave 0 routes them from LDS.
 template <bool F16>
-__global__ __launch_bounds__(256) void moe_gate_kernel(const void *w, const float *x, int n_embd, int n_expert,
-                                                       int n_used, int32_t *ids, float *weights) {
-    __shared__ float lds_logit[64];
+__device__ inline void router_logits(const void *w, const float *x, int n_embd, int n_expert, float *lds_logit) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int t = blockIdx.x;
     const int nc = n_embd / 8;
-    const floatx4 *xr = reinterpret_cast<const floatx4 *>(x + (int64_t)t * n_embd);
+    const floatx4 *xr = reinterpret_cast<const floatx4 *>(x);
     for (int e0 = wave; e0 < n_expert; e0 += 2 * kLayerWaves) {
         const int e1 = min(e0 + kLayerWaves, n_expert - 1);  // two rows per pass (clamped, stored once)
         float a0 = 0.0f, a1 = 0.0f;
@@ -276,8 +285,43 @@ __global__ __launch_bounds__(256) void moe_gate_kernel(const void *w, const floa
             if (e0 + kLayerWaves < n_expert) lds_logit[e0 + kLayerWaves] = a1;
         }
     }
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void moe_gate_kernel(const void *w, const float *x, int n_embd, int n_expert,
+                                                       int n_used, int32_t *ids, float *weights) {
+    __shared__ float lds_logit[64];
+    const int t = blockIdx.x;
+    router_logits<F16>(w, x + (int64_t)t * n_embd, n_embd, n_expert, lds_logit);
     __syncthreads();
-    if (wave == 0)
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64)
+        route_wave(lds_logit[min(lane, n_expert - 1)], lane, n_expert, n_used, ids + (int64_t)t * n_used,
+                   weights + (int64_t)t * n_used);
+}
+
+// ffn_norm, the router product and the routing in one launch
+// (engine.cpp:1908-1925): the workgroup normalises its token's row
+// (norm_row, written to y for the experts and kept in LDS), then computes the
+// logits from the LDS copy and routes them as moe_gate_kernel does.  One
+// launch less than rms_norm + gate; bit-identical to that pair.
+constexpr int kNormGateMaxEmbd = 8192;
+template <bool F16>
+__global__ __launch_bounds__(kNormThreads) void moe_norm_gate_kernel(const float *x, const float *nw, float eps,
+                                                                     const void *w, int n_embd, int n_expert,
+                                                                     int n_used, float *y, int32_t *ids,
+                                                                     float *weights) {
+    static_assert(kNormThreads == 64 * kLayerWaves, "the router product's waves");
+    __shared__ double part[kNormThreads / 64];
+    __shared__ __attribute__((aligned(16))) float lds_x[kNormGateMaxEmbd];
+    __shared__ float lds_logit[64];
+    const int t = blockIdx.x;
+    norm_row(x + (int64_t)t * n_embd, nw, y + (int64_t)t * n_embd, lds_x, n_embd, eps, part);
+    __syncthreads();
+    router_logits<F16>(w, lds_x, n_embd, n_expert, lds_logit);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64)
         route_wave(lds_logit[min(lane, n_expert - 1)], lane, n_expert, n_used, ids + (int64_t)t * n_used,
                    weights + (int64_t)t * n_used);
 }
@@ -448,6 +492,95 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
     }
 }
 
+// ---- Q/K/V product + RoPE + KV append ----------------------------------------
+
+// The stacked Q/K/V product (engine.cpp:1883-1885), RoPE NORMAL of Q and K
+// (:1892-1897) and the KV append (:1646-1656) in one launch, for decode
+// tokens: gemv_kernel's arithmetic for the rows (wave w < 4 of block b owns
+// row 4b + w, so a workgroup holds two whole RoPE pairs); a fifth wave
+// meanwhile computes the two pairs' cos / sin and destination rows
+// (rope_append_kernel's rope_cos_sin and row_ptr), so only the rotation
+// (rope_rotate) and the stores follow the products.  Rows [0, n_q) are Q
+// (written rotated to q, or as computed for a token with seq or pos < 0,
+// which rope_append_kernel leaves alone), then n_kv K rows, then n_kv V rows;
+// F16 caches round to nearest even, F32 store as is.  Grid (n_out / 4, n_tok).
+struct QkvRopeParams {
+    const void *w;     // [n_out][n_in]
+    const float *x;    // [n_tok][n_in]
+    float *q;          // [n_tok][n_q]
+    int n_in, n_out, n_q;
+    float theta_scale;
+    AppendParams ap;   // k / v unused
+};
+constexpr int kQkvThreads = 64 * (kLayerWaves + 1);
+template <bool F16, int KVT>
+__global__ __launch_bounds__(kQkvThreads) void qkv_rope_append_kernel(QkvRopeParams p) {
+    __shared__ float lds_y[kLayerWaves];
+    __shared__ float lds_cs[2][2];      // per pair: cos, sin
+    __shared__ uint8_t *lds_dst[2];     // per pair: the K or V row (null: not written)
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tok = blockIdx.y;
+    const int hd = p.ap.head_dim;
+    const int n_kv = p.ap.n_head_kv * hd;
+    if (wave == kLayerWaves) {
+        if (lane < 2) {
+            const int row = (int)blockIdx.x * kLayerWaves + 2 * lane;  // the pair's first row
+            const bool is_q = row < p.n_q, is_k = !is_q && row < p.n_q + n_kv;
+            const int r = is_q ? row : row - p.n_q - (is_k ? 0 : n_kv);
+            const int ps = p.ap.pos[tok];
+            const bool valid = ps >= 0 && p.ap.seq[tok] >= 0;
+            float c = 1.0f, sn = 0.0f;
+            if (valid && (is_q || is_k)) rope_cos_sin(ps, (r % hd) / 2, p.theta_scale, c, sn);
+            lds_cs[lane][0] = c;
+            lds_cs[lane][1] = sn;
+            lds_dst[lane] = is_q ? nullptr : row_ptr(p.ap, is_k ? 0 : 1, tok, r / hd);
+        }
+    } else {
+        const int row = (int)blockIdx.x * kLayerWaves + wave;  // < n_out (n_out % 4 == 0)
+        const int nc = p.n_in / 8;
+        const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)tok * p.n_in);
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int c = lane; c < nc; c += 64) {
+            if constexpr (F16) {
+                const half8 *W = static_cast<const half8 *>(p.w);
+                acc = dot8(W[(int64_t)row * nc + c], to_half8(xr[2 * c], xr[2 * c + 1]), acc);
+            } else {
+                const floatx4 *W = static_cast<const floatx4 *>(p.w);
+                acc = dot8(W[((int64_t)row * nc + c) * 2], W[((int64_t)row * nc + c) * 2 + 1], xr[2 * c],
+                           xr[2 * c + 1], acc);
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) lds_y[wave] = acc;
+    }
+    __syncthreads();
+    if (wave == kLayerWaves || lane != 0) return;
+    const int row = (int)blockIdx.x * kLayerWaves + wave;
+    const int pr = wave >> 1;
+    const bool is_q = row < p.n_q, is_k = !is_q && row < p.n_q + n_kv;
+    const int ps = p.ap.pos[tok];
+    const bool valid = ps >= 0 && p.ap.seq[tok] >= 0;
+    float y = lds_y[wave];
+    if (valid && (is_q || is_k)) {
+        float x0 = lds_y[wave & ~1], x1 = lds_y[wave | 1];
+        rope_rotate(x0, x1, lds_cs[pr][0], lds_cs[pr][1]);
+        y = (wave & 1) ? x1 : x0;
+    }
+    if (is_q) {
+        p.q[(int64_t)tok * p.n_q + row] = y;
+        return;
+    }
+    uint8_t *dst = lds_dst[pr];
+    if (dst == nullptr) return;
+    const int d = (row - p.n_q - (is_k ? 0 : n_kv)) % hd;
+    if constexpr (KVT == SFA_KV_F16)
+        reinterpret_cast<_Float16 *>(dst)[d] = (_Float16)y;
+    else
+        reinterpret_cast<float *>(dst)[d] = y;
+}
+
 // ---- host side -------------------------------------------------------------------
 
 static int grid_x(int n) { return (n + kRowsPerBlock - 1) / kRowsPerBlock; }
@@ -547,6 +680,87 @@ SFA_API int sfa_moe_gate(const void *gate_inp, int32_t w_type, const float *x, i
         else
             hipLaunchKernelGGL(sfa::moe_gate_kernel<false>, dim3(n_rows), dim3(256), 0, s, gate_inp, x, n_embd,
                                n_expert, n_used, ids, weights);
+        return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
+SFA_API int sfa_moe_norm_gate(const float *x, const float *norm_weight, float eps, const void *gate_inp,
+                              int32_t w_type, int32_t n_rows, int32_t n_embd, int32_t n_expert, int32_t n_used,
+                              float *y, int32_t *ids, float *weights, void *stream) {
+    try {
+        if (x == nullptr || norm_weight == nullptr || gate_inp == nullptr || y == nullptr || ids == nullptr ||
+            weights == nullptr)
+            return SFA_ERR_INVALID_ARGUMENT;
+        if (n_rows < 0 || n_embd <= 0 || !(eps >= 0.0f) || n_expert <= 0 || n_used <= 0 || n_used > n_expert)
+            return SFA_ERR_INVALID_ARGUMENT;
+        if (!sfa::weight_type_ok(w_type) || n_embd % 8 != 0 || n_embd > sfa::kNormGateMaxEmbd || n_expert > 64)
+            return SFA_ERR_UNSUPPORTED;
+        if (n_rows == 0) return SFA_OK;
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        if (w_type == SFA_KV_F16)
+            hipLaunchKernelGGL(sfa::moe_norm_gate_kernel<true>, dim3(n_rows), dim3(sfa::kNormThreads), 0, s, x,
+                               norm_weight, eps, gate_inp, n_embd, n_expert, n_used, y, ids, weights);
+        else
+            hipLaunchKernelGGL(sfa::moe_norm_gate_kernel<false>, dim3(n_rows), dim3(sfa::kNormThreads), 0, s, x,
+                               norm_weight, eps, gate_inp, n_embd, n_expert, n_used, y, ids, weights);
+        return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
+}
+
+SFA_API int sfa_qkv_rope_kv_append(const sfa_kv_desc *kv, const void *w_qkv, int32_t w_type, const float *x,
+                                   int32_t n_embd, float *q, const int32_t *seq, const int32_t *pos,
+                                   int32_t n_tok, const int32_t *page_table, int32_t max_pages,
+                                   float freq_base, void *stream) {
+    try {
+        if (kv == nullptr || w_qkv == nullptr || x == nullptr || q == nullptr || seq == nullptr ||
+            pos == nullptr || page_table == nullptr)
+            return SFA_ERR_INVALID_ARGUMENT;
+        const int rc = sfa_kv_desc_check(kv);
+        if (rc != SFA_OK) return rc;
+        if (n_tok < 0 || n_embd <= 0 || max_pages <= 0 || !(freq_base > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
+        if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_F32) return SFA_ERR_UNSUPPORTED;
+        if (!sfa::weight_type_ok(w_type) || n_embd % 8 != 0) return SFA_ERR_UNSUPPORTED;
+        if (n_tok == 0) return SFA_OK;
+        sfa::QkvRopeParams p;
+        p.w = w_qkv;
+        p.x = x;
+        p.q = q;
+        p.n_in = n_embd;
+        p.n_q = kv->n_head * kv->head_dim;
+        p.n_out = p.n_q + 2 * kv->n_head_kv * kv->head_dim;
+        p.theta_scale = powf(freq_base, -2.0f / (float)kv->head_dim);  // ggml: powf(base, -2/n_dims)
+        sfa::AppendParams &a = p.ap;
+        a.k_pages = static_cast<uint8_t *>(kv->k_pages);
+        a.v_pages = static_cast<uint8_t *>(kv->v_pages);
+        a.k_cold = static_cast<uint8_t *>(kv->k_cold);
+        a.v_cold = static_cast<uint8_t *>(kv->v_cold);
+        a.row_bytes = (int)sfa_row_bytes(kv);
+        a.page_bytes = (int64_t)a.row_bytes * kv->n_head_kv * kv->page_size;
+        a.n_pages = kv->n_pages;
+        a.n_cold = kv->n_cold_pages;
+        a.page_size = kv->page_size;
+        a.n_head_kv = kv->n_head_kv;
+        a.head_dim = kv->head_dim;
+        a.k = a.v = nullptr;
+        a.seq = seq;
+        a.pos = pos;
+        a.n_tok = n_tok;
+        a.page_table = page_table;
+        a.max_pages = max_pages;
+        const dim3 grid((unsigned)(p.n_out / sfa::kLayerWaves), (unsigned)n_tok);
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        const bool f16w = w_type == SFA_KV_F16;
+        if (kv->kv_type == SFA_KV_F16) {
+            if (f16w) hipLaunchKernelGGL((sfa::qkv_rope_append_kernel<true, SFA_KV_F16>), grid, dim3(sfa::kQkvThreads), 0, s, p);
+            else hipLaunchKernelGGL((sfa::qkv_rope_append_kernel<false, SFA_KV_F16>), grid, dim3(sfa::kQkvThreads), 0, s, p);
+        } else {
+            if (f16w) hipLaunchKernelGGL((sfa::qkv_rope_append_kernel<true, SFA_KV_F32>), grid, dim3(sfa::kQkvThreads), 0, s, p);
+            else hipLaunchKernelGGL((sfa::qkv_rope_append_kernel<false, SFA_KV_F32>), grid, dim3(sfa::kQkvThreads), 0, s, p);
+        }
         return hipGetLastError() == hipSuccess ? SFA_OK : SFA_ERR_RUNTIME;
     } catch (...) {
         return SFA_ERR_RUNTIME;

@@ -14,7 +14,7 @@ import torch
 from . import _lib
 from ._lib import SFA_KV_F16, SFA_KV_F32
 
-__all__ = ["rms_norm", "mul_mat_vec", "moe_route", "moe_gate", "moe_ffn", "weight_type"]
+__all__ = ["rms_norm", "mul_mat_vec", "moe_route", "moe_gate", "moe_norm_gate", "moe_ffn", "weight_type"]
 
 
 def _stream(stream) -> int:
@@ -96,6 +96,31 @@ def moe_gate(gate_inp: torch.Tensor, x: torch.Tensor, n_used: int, ids: torch.Te
                                         n_expert, n_used, ids.data_ptr(), weights.data_ptr(), _stream(stream)),
                "sfa_moe_gate")
     return ids, weights
+
+
+def moe_norm_gate(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, gate_inp: torch.Tensor, n_used: int,
+                  out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
+                  weights: torch.Tensor | None = None, stream=None):
+    """rms_norm(x) * norm_weight and the routing of the normed rows in one
+    launch: -> (y f32 [n_rows, n_embd], ids int32, weights f32 [n_rows, n_used]),
+    equal bit for bit to rms_norm followed by moe_gate."""
+    _f32(x, "x")
+    _f32(norm_weight, "norm_weight")
+    n_rows, n_embd = x.shape
+    n_expert = gate_inp.shape[0]
+    assert gate_inp.is_contiguous() and gate_inp.shape == (n_expert, n_embd)
+    assert norm_weight.shape == (n_embd,)
+    if out is None:
+        out = torch.empty_like(x)
+    if ids is None:
+        ids = torch.empty((n_rows, n_used), dtype=torch.int32, device=x.device)
+    if weights is None:
+        weights = torch.empty((n_rows, n_used), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.load().sfa_moe_norm_gate(x.data_ptr(), norm_weight.data_ptr(), float(eps), gate_inp.data_ptr(),
+                                             weight_type(gate_inp), n_rows, n_embd, n_expert, n_used,
+                                             out.data_ptr(), ids.data_ptr(), weights.data_ptr(), _stream(stream)),
+               "sfa_moe_norm_gate")
+    return out, ids, weights
 
 
 def moe_ffn(x: torch.Tensor, residual: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,

@@ -132,6 +132,29 @@ class PagedKV:
                                           int(page_table.shape[-1]), float(freq_base), _stream(stream)),
                    "sfa_rope_kv_append")
 
+    def qkv_rope_append(self, layer: int, w_qkv: torch.Tensor, x: torch.Tensor, seq: torch.Tensor,
+                        pos: torch.Tensor, page_table: torch.Tensor, freq_base: float,
+                        q: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """The stacked Q/K/V product of x [n_tok, n_embd] (w_qkv
+        [(Hq + 2 Hkv) hd, n_embd], f32 or f16), RoPE and the append in one
+        launch -> q [n_tok, Hq, hd] rotated."""
+        from .layer import weight_type
+        n_tok = int(seq.numel())
+        n_embd = int(x.shape[-1])
+        assert x.is_contiguous() and x.dtype == torch.float32 and x.shape == (n_tok, n_embd)
+        assert w_qkv.is_contiguous() and w_qkv.shape == ((self.n_head + 2 * self.n_head_kv) * self.head_dim, n_embd)
+        if q is None:
+            q = torch.empty((n_tok, self.n_head, self.head_dim), dtype=torch.float32, device=x.device)
+        assert q.is_contiguous() and q.dtype == torch.float32 and q.shape == (n_tok, self.n_head, self.head_dim)
+        lib = _lib.load()
+        d = self.desc(layer)
+        _lib.check(lib.sfa_qkv_rope_kv_append(ctypes.byref(d), w_qkv.data_ptr(), weight_type(w_qkv), x.data_ptr(),
+                                              n_embd, q.data_ptr(), seq.data_ptr(), pos.data_ptr(), n_tok,
+                                              page_table.data_ptr(), int(page_table.shape[-1]), float(freq_base),
+                                              _stream(stream)),
+                   "sfa_qkv_rope_kv_append")
+        return q
+
     def decode(self, layer: int, q: torch.Tensor, page_table: torch.Tensor, seq_len: torch.Tensor,
                max_seq_len: int, kv_lo: torch.Tensor | None = None, out: torch.Tensor | None = None,
                scale: float | None = None, stream=None, split_end_event=None) -> torch.Tensor:

@@ -202,11 +202,12 @@ class TinyMoeGpu(TinyMoe):
     """The whole forward on the GPU through libsfa.so, the decode layer of
     build_router_segment + build_expert_segment (engine.cpp:1877-1986) op by
     op: rms_norm * attn_norm; one product for Q, K and V (the three weights
-    stacked row-wise: the same dot products, one launch); RoPE of Q and K fused
-    with the KV append; the decode (one token) or the causal prefill (a
+    stacked row-wise: the same dot products, one launch) with RoPE of Q and K
+    and the KV append in the same launch (Q8_0 caches: the product, then RoPE
+    fused with the append); the decode (one token) or the causal prefill (a
     chunk), then the wo product with the residual added in the same pass;
-    rms_norm * ffn_norm; the router product; softmax top-k
-    routing; the SwiGLU experts with their weighted sum and the residual; the
+    rms_norm * ffn_norm with the router product and the softmax top-k
+    routing (one launch); the SwiGLU experts with their weighted sum and the residual; the
     output head.  Token ids go in and the last row's logits come out; nothing
     else crosses the host link.  ``weight_dtype`` float16 rounds the weights
     (a different model, for timing); float32 is the reference's."""
@@ -243,6 +244,7 @@ class TinyMoeGpu(TinyMoe):
 
     def forward(self, tokens, pos0: int) -> np.ndarray:
         from . import layer as ops
+        from .paged_kv import SFA_KV_F16, SFA_KV_F32
         torch, cfg = self.torch, self.cfg
         dev = self.device
         tok = torch.as_tensor(np.asarray(tokens, np.int64), device=dev)
@@ -254,18 +256,22 @@ class TinyMoeGpu(TinyMoe):
         x = self.embd.index_select(0, tok)                                  # get_rows (engine.cpp:2712)
         for il, L in enumerate(self.layers):
             cur = ops.rms_norm(x, L["attn_norm"], cfg.rms_eps)
-            qkv = ops.mul_mat_vec(L["wqkv"], cur)
-            q = qkv[:, :Hq * hd].contiguous().view(T, Hq, hd)
-            k = qkv[:, Hq * hd:(Hq + Hkv) * hd].contiguous().view(T, Hkv, hd)
-            v = qkv[:, (Hq + Hkv) * hd:].contiguous().view(T, Hkv, hd)
-            self.kv.rope_append(il, q, k, v, seq, pos, self.pt, cfg.freq_base)
+            if self.kv.kv_type in (SFA_KV_F16, SFA_KV_F32):
+                # the product, RoPE and the append in one launch
+                q = self.kv.qkv_rope_append(il, L["wqkv"], cur, seq, pos, self.pt, cfg.freq_base)
+            else:  # Q8_0: a block spans 16 RoPE pairs, so the product and the append are separate
+                qkv = ops.mul_mat_vec(L["wqkv"], cur)
+                q = qkv[:, :Hq * hd].contiguous().view(T, Hq, hd)
+                k = qkv[:, Hq * hd:(Hq + Hkv) * hd].contiguous().view(T, Hkv, hd)
+                v = qkv[:, (Hq + Hkv) * hd:].contiguous().view(T, Hkv, hd)
+                self.kv.rope_append(il, q, k, v, seq, pos, self.pt, cfg.freq_base)
             if T == 1:
                 attn = self.kv.decode(il, q, self.pt, sl, self.n_ctx)
             else:
                 attn = self.kv.prefill(il, q, self.pt[0], pos0)
             ffn_inp = ops.mul_mat_vec(L["wo"], attn, residual=x)
-            cur = ops.rms_norm(ffn_inp, L["ffn_norm"], cfg.rms_eps)
-            ids, wts = ops.moe_gate(L["gate_inp"], cur, cfg.n_expert_used)
+            cur, ids, wts = ops.moe_norm_gate(ffn_inp, L["ffn_norm"], cfg.rms_eps, L["gate_inp"],
+                                              cfg.n_expert_used)
             need = T * cfg.n_expert_used * cfg.n_ff * 4
             if self._moe_ws is None or self._moe_ws.numel() < need:
                 self._moe_ws = torch.empty(need, dtype=torch.uint8, device=dev)

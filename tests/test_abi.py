@@ -45,6 +45,22 @@ def test_layer_entry_points_validate_on_the_host():
     assert lib.sfa_mul_mat_vec(p, F32, None, None, p, 1, 128, 64, None) == bad
     assert lib.sfa_moe_route(p, 1, 65, 2, p, p, None) == uns                     # > 64 experts
     assert lib.sfa_moe_route(p, 1, 8, 9, p, p, None) == bad                      # n_used > n_expert
+    assert lib.sfa_moe_norm_gate(p, p, 1e-5, p, F32, 1, 8200, 8, 2, p, p, p, None) == uns  # row past LDS
+    assert lib.sfa_moe_norm_gate(p, p, 1e-5, p, F32, 1, 4100, 8, 2, p, p, p, None) == uns  # n_embd % 8
+    assert lib.sfa_moe_norm_gate(p, p, 1e-5, p, F16, 1, 4096, 65, 2, p, p, p, None) == uns  # > 64 experts
+    assert lib.sfa_moe_norm_gate(p, p, 1e-5, p, 8, 1, 4096, 8, 2, p, p, p, None) == uns    # Q8_0 weights
+    assert lib.sfa_moe_norm_gate(p, p, 1e-5, p, F32, 1, 4096, 8, 9, p, p, p, None) == bad  # n_used > n_expert
+    assert lib.sfa_moe_norm_gate(None, p, 1e-5, p, F32, 1, 4096, 8, 2, p, p, p, None) == bad
+    assert lib.sfa_moe_norm_gate(p, p, -1.0, p, F32, 1, 4096, 8, 2, p, p, p, None) == bad  # eps < 0
+    assert lib.sfa_moe_norm_gate(p, p, 1e-5, p, F32, 0, 4096, 8, 2, p, p, p, None) == _lib.SFA_OK
+    d = desc()
+    assert lib.sfa_qkv_rope_kv_append(ctypes.byref(desc(kv_type=_lib.SFA_KV_Q8_0)), p, F16, p, 4096, p, p, p, 1,
+                                      p, 16, 1e6, None) == uns                   # Q8_0 cache
+    assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4100, p, p, p, 1, p, 16, 1e6, None) == uns
+    assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, 8, p, 4096, p, p, p, 1, p, 16, 1e6, None) == uns
+    assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4096, p, p, p, 1, p, 16, 0.0, None) == bad
+    assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4096, None, p, p, 1, p, 16, 1e6, None) == bad
+    assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4096, p, p, p, 0, p, 16, 1e6, None) == _lib.SFA_OK
     assert lib.sfa_moe_workspace_bytes(2, 2, 512) == 2 * 2 * 512 * 4
     assert lib.sfa_moe_workspace_bytes(0, 2, 512) == 0
     ws = lib.sfa_moe_workspace_bytes(1, 2, 512)

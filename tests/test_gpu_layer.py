@@ -225,6 +225,30 @@ def test_layer_ops_in_a_graph(gpu):
 
 
 @pytest.mark.parametrize("wdtype", ["f32", "f16"])
+@pytest.mark.parametrize("n_rows,n_embd,n_expert,k", [(1, 4096, 8, 2), (3, 256, 8, 2), (2, 512, 64, 6),
+                                                      (1, 128, 3, 3), (2, 8192, 8, 2)])
+def test_moe_norm_gate_equals_norm_then_gate(gpu, wdtype, n_rows, n_embd, n_expert, k):
+    """ffn_norm + router + routing in one launch gives the bits of sfa_rms_norm
+    then sfa_moe_gate: the normed rows, the ids and the weights; and the normed
+    rows match the float64 restatement of ggml's rms_norm."""
+    from strataflow_amd import layer
+    rng = np.random.default_rng(7 * n_embd + n_expert)
+    w = (rng.standard_normal((n_expert, n_embd)) / np.sqrt(n_embd)).astype(np.float32)
+    if wdtype == "f16":
+        w = w.astype(np.float16)
+    x = (3.0 * rng.standard_normal((n_rows, n_embd))).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(n_embd)).astype(np.float32)
+    tw, tx, tnw = _t(w, gpu), _t(x, gpu), _t(nw, gpu)
+    y, ids, wts = layer.moe_norm_gate(tx, tnw, 1e-5, tw, k)
+    y2 = layer.rms_norm(tx, tnw, 1e-5)
+    ids2, wts2 = layer.moe_gate(tw, y2, k)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+    assert np.array_equal(ids.cpu().numpy(), ids2.cpu().numpy())
+    assert np.array_equal(wts.cpu().numpy().view(np.uint32), wts2.cpu().numpy().view(np.uint32))
+    np.testing.assert_allclose(y.cpu().numpy(), _rms_ref(x, nw, 1e-5), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("wdtype", ["f32", "f16"])
 @pytest.mark.parametrize("n_rows,n_embd,n_expert,k", [(1, 4096, 8, 2), (3, 256, 8, 2), (2, 512, 64, 6), (1, 128, 3, 3)])
 def test_moe_gate_equals_product_then_route(gpu, wdtype, n_rows, n_embd, n_expert, k):
     """The fused router product + routing gives the bits of sfa_mul_mat_vec then

@@ -178,3 +178,48 @@ def test_rope_append_rejects_bad_arguments(gpu):
     rc = lib.sfa_rope_kv_append(ctypes.byref(d), None, None, x.data_ptr(), i.data_ptr(),
                                 i.data_ptr(), 1, pt.data_ptr(), 2, 1e4, None)
     assert rc == _lib.SFA_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("kv_type", [F32, F16])
+@pytest.mark.parametrize("wdtype", ["f32", "f16"])
+@pytest.mark.parametrize("shape,n_embd", [((32, 8, 128), 4096), ((8, 4, 32), 256), ((16, 8, 64), 512)])
+def test_qkv_rope_append_equals_product_then_rope_append(gpu, kv_type, wdtype, shape, n_embd):
+    """sfa_qkv_rope_kv_append gives the bits of sfa_mul_mat_vec followed by
+    sfa_rope_kv_append on its Q, K and V parts: the rotated Q and every byte of
+    both pools, with a skipped token (seq -1, Q as computed) and a token whose
+    page id lies outside the pool (Q rotated, nothing written)."""
+    import torch
+    from strataflow_amd import layer
+    from strataflow_amd.paged_kv import PagedKV
+    Hq, Hkv, hd = shape
+    rng = np.random.default_rng(11 * hd + kv_type + n_embd)
+    ps, max_pages, n_seq = 64, 8, 2
+    n_pages = n_seq * max_pages + 2
+    seq, pos = _tokens(rng, n_seq, 6, ps, max_pages)
+    pt = rng.permutation(n_pages)[:n_seq * max_pages].reshape(n_seq, max_pages).astype(np.int32)
+    seq[1] = -1
+    pt[seq[2], pos[2] // ps] = n_pages + 5
+    n = seq.size
+    n_out = (Hq + 2 * Hkv) * hd
+    w = (rng.standard_normal((n_out, n_embd)) / np.sqrt(n_embd)).astype(np.float32)
+    if wdtype == "f16":
+        w = w.astype(np.float16)
+    x = rng.standard_normal((n, n_embd)).astype(np.float32)
+    base = 1e6 if hd == 128 else 1e4
+    tw, tx = torch.from_numpy(w).to(gpu), torch.from_numpy(x).to(gpu)
+    ts, tp, tpt = (torch.from_numpy(a).to(gpu) for a in (seq, pos, pt))
+    a = PagedKV(1, Hq, Hkv, hd, kv_type, ps, n_pages, device=gpu)
+    b = PagedKV(1, Hq, Hkv, hd, kv_type, ps, n_pages, device=gpu)
+    qa = a.qkv_rope_append(0, tw, tx, ts, tp, tpt, base)
+    qkv = layer.mul_mat_vec(tw, tx)
+    qb = qkv[:, :Hq * hd].contiguous().view(n, Hq, hd)
+    kb = qkv[:, Hq * hd:(Hq + Hkv) * hd].contiguous().view(n, Hkv, hd)
+    vb = qkv[:, (Hq + Hkv) * hd:].contiguous().view(n, Hkv, hd)
+    b.rope_append(0, qb, kb, vb, ts, tp, tpt, base)
+    torch.cuda.synchronize()
+    assert np.array_equal(qa.cpu().numpy().view(np.uint32), qb.cpu().numpy().view(np.uint32))
+    assert np.array_equal(a.k[0].cpu().numpy(), b.k[0].cpu().numpy())
+    assert np.array_equal(a.v[0].cpu().numpy(), b.v[0].cpu().numpy())
+    # the skipped token's Q is the product as computed, and something was written
+    assert np.array_equal(qa[1].cpu().numpy().ravel(), qkv[1, :Hq * hd].cpu().numpy())
+    assert a.k[0].abs().sum().item() > 0
