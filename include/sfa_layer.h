@@ -90,8 +90,8 @@ SFA_API int sfa_moe_norm_gate(const float *x, const float *norm_weight, float ep
  *           token with seq or pos < 0, whose K/V are not written)
  *   seq, pos, page_table, max_pages, freq_base : as sfa_rope_kv_append.
  * F16 and F32 caches; SFA_ERR_UNSUPPORTED for Q8_0 (a block spans 16 RoPE
- * pairs: use the two calls).  One workgroup reads the whole weight matrix per
- * token, so this is the decode path; a long chunk is better served by
+ * pairs: use the two calls) and for n_tok > 65535.  The weight matrix is read
+ * once per token, so this is the decode path; a long chunk is better served by
  * sfa_mul_mat_vec + sfa_rope_kv_append. */
 SFA_API int sfa_qkv_rope_kv_append(const sfa_kv_desc *kv, const void *w_qkv, int32_t w_type,
                                    const float *x, int32_t n_embd, float *q, const int32_t *seq,

@@ -723,7 +723,7 @@ SFA_API int sfa_qkv_rope_kv_append(const sfa_kv_desc *kv, const void *w_qkv, int
         if (rc != SFA_OK) return rc;
         if (n_tok < 0 || n_embd <= 0 || max_pages <= 0 || !(freq_base > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
         if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_F32) return SFA_ERR_UNSUPPORTED;
-        if (!sfa::weight_type_ok(w_type) || n_embd % 8 != 0) return SFA_ERR_UNSUPPORTED;
+        if (!sfa::weight_type_ok(w_type) || n_embd % 8 != 0 || n_tok > 65535) return SFA_ERR_UNSUPPORTED;
         if (n_tok == 0) return SFA_OK;
         sfa::QkvRopeParams p;
         p.w = w_qkv;

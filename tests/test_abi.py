@@ -61,6 +61,7 @@ def test_layer_entry_points_validate_on_the_host():
     assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4096, p, p, p, 1, p, 16, 0.0, None) == bad
     assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4096, None, p, p, 1, p, 16, 1e6, None) == bad
     assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4096, p, p, p, 0, p, 16, 1e6, None) == _lib.SFA_OK
+    assert lib.sfa_qkv_rope_kv_append(ctypes.byref(d), p, F16, p, 4096, p, p, p, 70000, p, 16, 1e6, None) == uns
     assert lib.sfa_moe_workspace_bytes(2, 2, 512) == 2 * 2 * 512 * 4
     assert lib.sfa_moe_workspace_bytes(0, 2, 512) == 0
     ws = lib.sfa_moe_workspace_bytes(1, 2, 512)
