@@ -201,3 +201,89 @@ def test_pager_step_graph_replay(gpu, attend):
     assert st[key] - st0[key] >= 2 * B  # pages left the window during the replayed steps
     eager_p.close()
     graph_p.close()
+
+
+def test_decode_layer_graph_replay(gpu):
+    """A whole decode layer (two layers, small shape, f16 weights and cache)
+    through the fused launches: attn_norm, Q/K/V + RoPE + append, decode, wo +
+    residual, ffn_norm + gate, experts.  Captured once, replayed for several
+    tokens with the position rewritten in place, interleaved with the same
+    step run eagerly on a twin cache: the layer output and both pools equal
+    the eager ones bit for bit at every step."""
+    import torch
+    from strataflow_amd import layer as ops
+    from strataflow_amd import synth
+    from strataflow_amd.paged_kv import PagedKV
+    L, D, Hq, Hkv, hd, E, K, F, ps = 2, 512, 8, 4, 64, 4, 2, 1024, 64
+    n_ctx = 4 * ps
+    rng = np.random.default_rng(33)
+    n_pages = n_ctx // ps + 2
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(33)
+
+    def w(*shape):
+        return (torch.randn(shape, device=gpu, generator=gen) * 0.05).half().contiguous()
+
+    layers = [dict(attn_norm=1 + 0.1 * torch.randn(D, device=gpu, generator=gen),
+                   ffn_norm=1 + 0.1 * torch.randn(D, device=gpu, generator=gen),
+                   wqkv=w((Hq + 2 * Hkv) * hd, D), wo=w(D, Hq * hd), gate_inp=w(E, D),
+                   gate=w(E, F, D), up=w(E, F, D), down=w(E, D, F)) for _ in range(L)]
+    pt = torch.from_numpy(synth.page_tables(rng, [n_ctx], ps, n_pages)).to(gpu)
+    caches = [PagedKV(L, Hq, Hkv, hd, 1, ps, n_pages, device=gpu) for _ in range(2)]
+    # a shared history of 100 positions in both caches
+    hist = 100
+    hpos = torch.arange(hist, dtype=torch.int32, device=gpu)
+    hseq = torch.zeros(hist, dtype=torch.int32, device=gpu)
+    for il in range(L):
+        k = torch.randn((hist, Hkv, hd), device=gpu, generator=gen)
+        v = torch.randn((hist, Hkv, hd), device=gpu, generator=gen)
+        for kv in caches:
+            kv.append(il, k, v, hseq, hpos, pt)
+    x0 = torch.empty((1, D), device=gpu)
+    pos = torch.zeros(1, dtype=torch.int32, device=gpu)
+    seq = torch.zeros(1, dtype=torch.int32, device=gpu)
+    sl = torch.zeros(1, dtype=torch.int32, device=gpu)
+
+    def buffers():
+        return dict(x=torch.empty((1, D), device=gpu), cur=torch.empty((1, D), device=gpu),
+                    ffn=torch.empty((1, D), device=gpu), q=torch.empty((1, Hq, hd), device=gpu),
+                    attn=torch.empty((1, Hq * hd), device=gpu),
+                    ids=torch.empty((1, K), dtype=torch.int32, device=gpu), wts=torch.empty((1, K), device=gpu),
+                    ws=torch.empty(K * F * 4, dtype=torch.uint8, device=gpu))
+
+    def step(kv, b):
+        b["x"].copy_(x0)
+        for il, Ly in enumerate(layers):
+            ops.rms_norm(b["x"], Ly["attn_norm"], 1e-5, out=b["cur"])
+            kv.qkv_rope_append(il, Ly["wqkv"], b["cur"], seq, pos, pt, 1e4, q=b["q"])
+            kv.decode(il, b["q"], pt, sl, n_ctx, out=b["attn"])
+            ops.mul_mat_vec(Ly["wo"], b["attn"], residual=b["x"], out=b["ffn"])
+            ops.moe_norm_gate(b["ffn"], Ly["ffn_norm"], 1e-5, Ly["gate_inp"], K, out=b["cur"], ids=b["ids"],
+                              weights=b["wts"])
+            ops.moe_ffn(b["cur"], b["ffn"], b["ids"], b["wts"], Ly["gate"], Ly["up"], Ly["down"], out=b["x"],
+                        workspace=b["ws"])
+
+    bg, be = buffers(), buffers()
+    x0.copy_(torch.randn((1, D), device=gpu, generator=gen))
+    pos.fill_(hist)
+    sl.fill_(hist + 1)
+    step(caches[0], bg)  # warm-up (also the first token, in both caches)
+    step(caches[1], be)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(caches[0], bg)
+    torch.cuda.synchronize()
+    # the capture recorded without running: the next replay writes position hist + 1
+    for p in range(hist + 1, hist + 6):
+        x0.copy_(torch.randn((1, D), device=gpu, generator=gen))
+        pos.fill_(p)
+        sl.fill_(p + 1)
+        bg["x"].fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        step(caches[1], be)
+        torch.cuda.synchronize()
+        assert torch.equal(bg["x"].view(torch.int32), be["x"].view(torch.int32)), f"position {p}"
+        assert torch.isfinite(bg["x"]).all()
+        assert torch.equal(caches[0].k, caches[1].k) and torch.equal(caches[0].v, caches[1].v), f"position {p}"
