@@ -2073,8 +2073,12 @@ struct SplitPlan {
 // span of max_seq_len positions, which covers one tile more when a window start
 // is not tile-aligned, cut into kDecodeWaves-tile splits), at least B, rounded
 // up to a multiple of 8.  The device plan deals the slots out by length.
-SplitPlan plan_splits(int B, int Hkv, int max_seq_len, bool windowed, bool cols) {
-    const int slot_target = 2048 / (cols ? 1 : kDecodeWaves);
+// One sequence over a Q8_0 cache (`one_q8`) takes half the slots: one
+// workgroup per CU with twice the tiles per wave (Mixtral shape, per layer:
+// 32k 25.0 -> 24.2 us, 8k 13.0 -> 12.4 us; f16 at 32k gains nothing, and a
+// quarter of the slots leaves CUs idle: 35.0 us).
+SplitPlan plan_splits(int B, int Hkv, int max_seq_len, bool windowed, bool cols, bool one_q8) {
+    const int slot_target = cols ? 2048 : (one_q8 ? 1024 : 2048) / kDecodeWaves;
     const int tiles = ceil_div(max_seq_len, kTile);
     const int span_tiles = windowed ? ceil_div(max_seq_len - 1, kTile) + 1 : tiles;
     int row = (slot_target + Hkv - 1) / Hkv;
@@ -2117,8 +2121,8 @@ int cols_waves_of(int Hkv) {
 
 size_t decode_workspace_bytes(int B, int Hkv, int G, int HD, int max_seq_len) {
     // the larger row of both layouts, windowed (one tile more)
-    const SplitPlan a = plan_splits(B, Hkv, max_seq_len, true, false);
-    const SplitPlan c = plan_splits(B, Hkv, max_seq_len, true, true);
+    const SplitPlan a = plan_splits(B, Hkv, max_seq_len, true, false, false);
+    const SplitPlan c = plan_splits(B, Hkv, max_seq_len, true, true, false);
     const int row = a.split_row > c.split_row ? a.split_row : c.split_row;
     return (size_t)Hkv * row * G * (HD + 4) * sizeof(float);
 }
@@ -2217,7 +2221,8 @@ int decode_setup(const sfa_kv_desc *kv, const float *q, float *out, const int32_
         return SFA_ERR_UNSUPPORTED;
     if (kv->kv_type == SFA_KV_Q8_0 && HD < 64) return SFA_ERR_UNSUPPORTED;
     const bool cols = use_cols(kv->kv_type, HD, G, B, max_seq_len, kv_lo != nullptr);
-    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, kv_lo != nullptr, cols);
+    const SplitPlan sp = plan_splits(B, Hkv, max_seq_len, kv_lo != nullptr, cols,
+                                     kv->kv_type == SFA_KV_Q8_0 && B == 1);
 
     DecodeParams p;
     p.k_pages = static_cast<const uint8_t *>(kv->k_pages);
