@@ -211,19 +211,28 @@ def load_traffic() -> dict:
 def with_traffic(roofline: dict, key: str) -> dict:
     """Adds the profiled HBM bytes per launch and the rocprofv3 mean duration
     of the same kernel on the same workload, with the achieved rate and frac
-    computed from that mean (beside the live figures, which use HIP events
-    around back-to-back launches)."""
+    computed from that mean, beside the live figures (HIP events around
+    back-to-back launches).  For a decode split pass the profile splits its
+    dispatches into the back-to-back launches the live figure times (the
+    rocprof_* figures, like with like) and those inside the decode steps,
+    each followed by its merge pass (rocprof_*_in_step)."""
     t = load_traffic().get(key)
     if t:
         roofline["traffic"] = t.get("bytes_per_launch")
         roofline["traffic_source"] = f"profiles/traffic.json[{key}] (rocprofv3 FETCH_SIZE+WRITE_SIZE)"
         work = roofline.get("bytes_per_launch") or roofline.get("flop_per_launch")
-        if work and t.get("kernel_us_mean"):
-            ach = work / (t["kernel_us_mean"] * 1e-6) / (1e9 if roofline["unit"] == "GB/s" else 1e12)
-            roofline["rocprof_kernel_us_mean"] = t["kernel_us_mean"]
+        scale = 1e9 if roofline["unit"] == "GB/s" else 1e12
+        us = t.get("kernel_us_mean_back_to_back") or t.get("kernel_us_mean")
+        if work and us:
+            ach = work / (us * 1e-6) / scale
+            roofline["rocprof_kernel_us_mean"] = us
             roofline["rocprof_achieved"] = round(ach, 1)
             roofline["rocprof_frac"] = round(ach / roofline["peak"], 4)
             roofline["rocprof_source"] = t.get("profile") or "profiles/"
+            if t.get("kernel_us_mean_in_step"):
+                us_s = t["kernel_us_mean_in_step"]
+                roofline["rocprof_kernel_us_mean_in_step"] = us_s
+                roofline["rocprof_frac_in_step"] = round(work / (us_s * 1e-6) / scale / roofline["peak"], 4)
         for k in ("mfma_busy", "valu_busy", "lds_bank_conflict_frac"):
             if t.get(k) is not None:
                 roofline[f"rocprof_{k}"] = t[k]
@@ -903,6 +912,7 @@ def decode_fields(prefix: str, leg: dict, per: str = "us_per_layer_token") -> di
     roof = _g(leg, "roofline") or {}
     return {f"{prefix}_us": _g(leg, per), f"{prefix}_kernel_us": roof.get("kernel_us_mean"),
             f"{prefix}_frac": roof.get("frac"), f"{prefix}_rocprof_frac": roof.get("rocprof_frac"),
+            f"{prefix}_rocprof_frac_in_step": roof.get("rocprof_frac_in_step"),
             f"{prefix}_node_frac": roof.get("node_frac"), f"{prefix}_traffic_x": _traffic_x(roof),
             f"{prefix}_cpu_us": _g(leg, "cpu_baseline", "value"),
             f"{prefix}_cpu_us_1t": _g(leg, "cpu_baseline", "value_1_thread")}
@@ -916,6 +926,7 @@ def legs_summary(r: dict) -> dict:
     s = {"decode_f16_4k_us": r.get("value"), "decode_f16_4k_kernel_us": _g(r, "roofline", "kernel_us_mean"),
          "decode_f16_4k_frac": _g(r, "roofline", "frac"),
          "decode_f16_4k_rocprof_frac": _g(r, "roofline", "rocprof_frac"),
+         "decode_f16_4k_rocprof_frac_in_step": _g(r, "roofline", "rocprof_frac_in_step"),
          "decode_f16_4k_node_frac": _g(r, "roofline", "node_frac"),
          "decode_f16_4k_traffic_x": _traffic_x(r.get("roofline")),
          "decode_f16_4k_cpu_us": _g(r, "cpu_baseline", "value"),
