@@ -807,8 +807,8 @@ def rope_bench(torch, steps: int, seed: int):
 def host_info() -> dict:
     """CPU model, logical CPUs, the CPUs this process may run on and the
     thread count the CPU legs use (the affinity set, capped by OMP_NUM_THREADS
-    when the environment sets it: the GPU host allots a share of its cores to
-    each GPU)."""
+    when the environment sets it: a machine with several GPUs may give each
+    GPU's process a share of its cores)."""
     aff = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS", "")
     threads = min(aff, int(omp)) if omp.isdigit() and int(omp) > 0 else aff

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (liboracle.so, built from sfa_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and the bench's
-CPU-baseline leg as the checker.  The product path never imports it.
+CPU-baseline leg, to check results against.  The product path never imports it.
 Pools here are host numpy arrays [n_pages, page_bytes] (uint8) holding the same
 bytes as the device pools.
 """

@@ -1,7 +1,7 @@
 /*
  * sfa_oracle.c - CPU restatement of StrataFlow's attention node over the KV
  * cache.  TEST INFRASTRUCTURE ONLY: tests/, the smoke check and the bench's
- * CPU-baseline leg load this library as the checker.  The product path (the HIP
+ * CPU-baseline leg load this library to check results against.  The product path (the HIP
  * library) never links, loads or calls it.
  *
  * What it restates (reference files under StrataFlow's tree):

@@ -3,7 +3,7 @@
 ``python -m strataflow_amd.build`` compiles every ``csrc/*.hip`` with hipcc for
 gfx950 only and links ``strataflow_amd/libsfa.so`` (the attention library);
 ``host/`` (the C++ page manager over it) becomes ``strataflow_amd/libsfa_host.so``;
-it also builds ``oracle/liboracle.so`` (the test-side checker) with make.
+it also builds ``oracle/liboracle.so`` (the CPU oracle the tests compare against) with make.
 """
 from __future__ import annotations
 
