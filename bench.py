@@ -609,8 +609,9 @@ def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 128, 
 
         def layers():
             for layer in range(n_layer):
-                pager.append(layer, kb[layer], vb[layer])
-                pager.attend(layer, qb[layer], out[layer])
+                # the attention node with its append (one token per sequence,
+                # F16: fused into the split pass)
+                pager.append_attend(layer, kb[layer], vb[layer], qb[layer], out[layer])
 
         assert pager.begin(ones) == 0  # one warm step (not timed) opens a step
         layers()
@@ -676,7 +677,8 @@ def window_bench(torch, seed: int, steps: int = 128, lossless_steps: int = 128, 
             "us_per_layer_step": round(us, 3),
             "us_per_layer_token": round(us / B, 3),
             "tokens_per_s": round(B * 1e6 / (us * n_layer), 1),
-            "includes": "paging (plan + table update), KV append, split-K decode and merge",
+            "includes": "paging (plan + table update), KV append (fused into the split-K pass), "
+                        "split-K decode and merge",
             "pages_evicted": st["pages_evicted"], "pages_dropped": st["pages_dropped"],
             "hbm_bytes_per_layer_step": hbm + qo,
             "host_link_bytes_per_layer_step": link,

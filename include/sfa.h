@@ -161,6 +161,26 @@ SFA_API int sfa_attn_decode(const sfa_kv_desc *kv, const float *q, float *out,
                             int32_t B, int32_t max_seq_len, float scale,
                             void *workspace, size_t ws_bytes, void *stream);
 
+/* The whole attention node of one decode step, the append included
+ * (build_kv_attention, engine.cpp:1633-1762: ggml_cpy of Kcur/Vcur into the
+ * cache column at engine.cpp:1646-1656, then the attention): appends each
+ * sequence's new token and attends, in the same two passes as
+ * sfa_attn_decode.
+ *   k, v : [B][n_head_kv][head_dim] f32, K post-RoPE; token b goes to position
+ *          seq_len[b] - 1 of sequence b (no token where seq_len[b] is 0)
+ *   the rest as sfa_attn_decode; the pools are written (kv->k_pages / v_pages
+ *   and the cold pools, through the page table).
+ * Equals sfa_kv_append(k, v, seq = b, pos = seq_len[b] - 1) followed by
+ * sfa_attn_decode, bit for bit, pool bytes included (a position past the
+ * table, or on a page id that is not there, is skipped as the append skips
+ * it).  F16 caches only: SFA_ERR_UNSUPPORTED for F32 and Q8_0, whose callers
+ * issue the two calls. */
+SFA_API int sfa_attn_decode_append(const sfa_kv_desc *kv, const float *k, const float *v,
+                                   const float *q, float *out, const int32_t *page_table,
+                                   int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo,
+                                   int32_t B, int32_t max_seq_len, float scale, void *workspace,
+                                   size_t ws_bytes, void *stream);
+
 /* The two passes of sfa_attn_decode, for callers that schedule them apart
  * (e.g. to overlap the merge with other work, or to time the split-K pass):
  * sfa_attn_decode == sfa_attn_decode_split then sfa_attn_decode_merge on the

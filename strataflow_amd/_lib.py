@@ -36,6 +36,7 @@ EXPORTS = (
     "sfa_decode_workspace_bytes",
     "sfa_workspace_init",
     "sfa_attn_decode",
+    "sfa_attn_decode_append",
     "sfa_attn_decode_split",
     "sfa_attn_decode_merge",
     "sfa_attn_decode_noalloc",
@@ -118,6 +119,9 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_attn_decode.argtypes = [D, P, P, P, i32, P, P, i32, i32, ctypes.c_float, P,
                                     ctypes.c_size_t, P]
     lib.sfa_attn_decode.restype = ctypes.c_int
+    lib.sfa_attn_decode_append.argtypes = [D, P, P, P, P, P, i32, P, P, i32, i32, ctypes.c_float, P,
+                                           ctypes.c_size_t, P]
+    lib.sfa_attn_decode_append.restype = ctypes.c_int
     for name in ("sfa_attn_decode_split", "sfa_attn_decode_merge"):
         f = getattr(lib, name)
         f.argtypes = lib.sfa_attn_decode.argtypes
@@ -173,6 +177,7 @@ HOST_EXPORTS = (
     "sfa_pager_append",
     "sfa_pager_rope_append",
     "sfa_pager_attend",
+    "sfa_pager_append_attend",
     "sfa_pager_reset",
     "sfa_pager_stats_get",
     "sfa_pager_desc",
@@ -239,6 +244,8 @@ def load_host(path: Path | str | None = None) -> ctypes.CDLL:
     lib.sfa_pager_rope_append.restype = ctypes.c_int
     lib.sfa_pager_attend.argtypes = [P, i32, P, P, P]
     lib.sfa_pager_attend.restype = ctypes.c_int
+    lib.sfa_pager_append_attend.argtypes = [P, i32, P, P, P, P, P]
+    lib.sfa_pager_append_attend.restype = ctypes.c_int
     lib.sfa_pager_reset.argtypes = [P, i32, P]
     lib.sfa_pager_reset.restype = ctypes.c_int
     lib.sfa_pager_stats_get.argtypes = [P, ctypes.POINTER(SfaPagerStats)]

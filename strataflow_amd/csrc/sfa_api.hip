@@ -26,6 +26,10 @@ int workspace_init_launch(void *ws, size_t bytes, hipStream_t stream);
 int decode_noalloc_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32_t *page_table,
                           int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo, int32_t B,
                           int32_t max_seq_len, float scale, hipStream_t stream);
+int decode_append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const float *q,
+                         float *out, const int32_t *page_table, int32_t max_pages,
+                         const int32_t *seq_len, const int32_t *kv_lo, int32_t B, int32_t max_seq_len,
+                         float scale, void *workspace, size_t ws_bytes, hipStream_t stream);
 }  // namespace sfa
 
 namespace {
@@ -149,6 +153,23 @@ SFA_API int sfa_attn_decode(const sfa_kv_desc *kv, const float *q, float *out,
                             void *stream) {
     return decode_entry(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
                         workspace, ws_bytes, stream, 3);
+}
+
+SFA_API int sfa_attn_decode_append(const sfa_kv_desc *kv, const float *k, const float *v,
+                                   const float *q, float *out, const int32_t *page_table,
+                                   int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo,
+                                   int32_t B, int32_t max_seq_len, float scale, void *workspace,
+                                   size_t ws_bytes, void *stream) {
+    try {
+        const int rc = check_desc(kv);
+        if (rc != SFA_OK) return rc;
+        if (!(scale > 0.0f)) return SFA_ERR_INVALID_ARGUMENT;
+        return sfa::decode_append_launch(kv, k, v, q, out, page_table, max_pages, seq_len, kv_lo, B,
+                                         max_seq_len, scale, workspace, ws_bytes,
+                                         static_cast<hipStream_t>(stream));
+    } catch (...) {
+        return SFA_ERR_RUNTIME;
+    }
 }
 
 SFA_API int sfa_attn_decode_split(const sfa_kv_desc *kv, const float *q, float *out,

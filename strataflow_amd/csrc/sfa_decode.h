@@ -35,6 +35,14 @@ struct DecodeParams {
     int staged;           // Q8_0 batches: 1 = decode_q8_staged_kernel (kStagedKv kv heads per wave)
     float scale_log2;     // scale * log2(e)
     float *part;          // [Hkv][split_row][G][HD + 4]: one (o, m, l) record per slot
+    // fused append (F16 cache): sequence b's new token, [B][Hkv][HD] f32, at
+    // position seq_len[b] - 1; nullptr otherwise
+    const float *app_k;
+    const float *app_v;
+    uint8_t *app_k_pages;  // the writable pools (k_pages / v_pages above)
+    uint8_t *app_v_pages;
+    uint8_t *app_k_cold;
+    uint8_t *app_v_cold;
 };
 
 constexpr int kDecodeWaves = 4;

@@ -113,7 +113,16 @@ __device__ inline void split_merge(float (*lds_m)[G], float (*lds_l)[G], float (
 // wait before the first tile's K/V requests is for the page-id load alone
 // (the Q loads stay in flight): a load inside a branch would make the
 // compiler's wait at the join count every later load.
-template <int HD, int G, bool ONE>
+// APP: the fused append (sfa_attn_decode_append).  Sequence b's new token
+// (app_k / app_v [B][Hkv][HD] f32, at position seq_len[b] - 1) is written to
+// its page rounded to f16 by wave 0 of row slot b (every sequence has a slot
+// of that number: the row holds at least B), with loads issued in the
+// prologue and stores at the end; the wave that owns the token's tile reads
+// the page row before that store may have landed, so it takes the row from
+// its own copy of the token instead (the K operand rows and the V tile row
+// of that position).  Both round as the append kernel does, so the result
+// equals sfa_kv_append then sfa_attn_decode bit for bit.
+template <int HD, int G, bool ONE, bool APP = false>
 __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
     static_assert(G >= 1 && G <= 32 && (32 % G) == 0, "group size");
@@ -129,6 +138,8 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     __shared__ float lds_l[kDecodeWaves][G];
     __shared__ __attribute__((aligned(16))) _Float16 lds_q[G * HD];
     __shared__ float lds_o[kDecodeWaves][G][HD];
+    // APP: the owner wave's new K and V rows (f16), staged for its operand
+    __shared__ __attribute__((aligned(16))) _Float16 lds_new[APP ? kDecodeWaves : 1][2][APP ? HD : 8];
 
     // slot j of kv head kvh's row; (b_g, split_g) is the host's guess of its
     // sequence and split, used to start the first tile's loads before the
@@ -223,6 +234,19 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     // the window starts at the guessed tile's page: its id is lane 0's
     bool tile_ok = issue(t_guess, __builtin_amdgcn_readlane(pages.ids, 0));
 
+    // APP writer: sequence `slot`'s new row, two elements per lane (lanes
+    // past head_dim / 2 repeat the last pair); loads unconditional, behind
+    // the first tile's
+    constexpr int APL = HD / 2;  // lanes carrying a new row's element pairs
+    const int app_e = 2 * (lane < APL ? lane : APL - 1);
+    const int app_ws = slot < p.n_seq ? slot : p.n_seq - 1;
+    float2 app_wk{}, app_wv{};
+    if constexpr (APP) {
+        const int64_t o = ((int64_t)app_ws * Hkv + kvh) * HD + app_e;
+        app_wk = *reinterpret_cast<const float2 *>(p.app_k + o);
+        app_wv = *reinterpret_cast<const float2 *>(p.app_v + o);
+    }
+
     SlotPlan sp;
     bool active;
     if constexpr (ONE) {
@@ -235,6 +259,37 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     } else {
         active = plan(p, raw, slot, -1, lane, sp);
     }
+    // raw seq_len of sequence j (wave-uniform): lane j of the plan's loads
+    // holds it when the batch has at most 64 sequences
+    auto seq_len_of = [&](int j) -> int {
+        if constexpr (ONE) return one_n_kv;
+        else return p.n_seq <= kWave ? __builtin_amdgcn_readlane(raw.n_kv, j) : p.seq_len[j];
+    };
+    // the writer's row: position seq_len - 1 of sequence `slot`, skipped past
+    // the table or for a page that is not there, as the append kernel skips
+    // them; its page id is loaded now and the stores go out at the end
+    int app_pn = -1;
+    int32_t app_wid = -1;
+    if constexpr (APP) {
+        const int pn = seq_len_of(app_ws) - 1;
+        const int lp = pn < 0 ? 0 : pn / p.page_size;
+        app_pn = slot < p.n_seq && wave_u == 0 && pn >= 0 && lp < p.max_pages ? pn : -1;
+        app_wid = p.page_table[(int64_t)app_ws * p.max_pages + (lp < p.max_pages ? lp : p.max_pages - 1)];
+    }
+    auto app_write = [&]() {
+        if constexpr (APP) {
+            if (app_pn < 0) return;
+            uint8_t *kb = const_cast<uint8_t *>(
+                page_base(app_wid, p.app_k_pages, p.n_pages, p.app_k_cold, p.n_cold, p.page_bytes));
+            uint8_t *vb = const_cast<uint8_t *>(
+                page_base(app_wid, p.app_v_pages, p.n_pages, p.app_v_cold, p.n_cold, p.page_bytes));
+            if (kb == nullptr || vb == nullptr || lane >= APL) return;
+            const int lp = app_pn / p.page_size;
+            const int64_t off = ((int64_t)(app_pn - lp * p.page_size) * Hkv + kvh) * p.row_bytes + 2 * app_e;
+            *reinterpret_cast<half2v *>(kb + off) = half2v{(_Float16)app_wk.x, (_Float16)app_wk.y};
+            *reinterpret_cast<half2v *>(vb + off) = half2v{(_Float16)app_wv.x, (_Float16)app_wv.y};
+        }
+    };
     if (!active) {
         // an idle slot; the merge pass writes the output of a sequence
         // without tiles, or, for one sequence, the slot that would own it
@@ -242,6 +297,7 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
             float *out0 = p.out + (int64_t)kvh * G * HD;
             for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out0[i] = 0.0f;
         }
+        app_write();
         return;
     }
     const int b = sp.b;
@@ -263,6 +319,24 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     float *out_b = p.out + ((int64_t)b * p.n_head + (int64_t)kvh * G) * HD;
     int t = tile_lo + wave_u;
     if (t != t_guess || b != b_g) tile_ok = t < tile_hi ? issue(t, page_of(t)) : false;
+    // APP owner: the wave whose tiles include sequence b's new position (its
+    // last tile) keeps the token's row (two elements per lane) to put in place
+    // of the page row it loads
+    int t_new = -1, r_new = 0;
+    float2 app_ok{}, app_ov{};
+    if constexpr (APP) {
+        const int64_t o = ((int64_t)b * Hkv + kvh) * HD + app_e;
+        app_ok = *reinterpret_cast<const float2 *>(p.app_k + o);
+        app_ov = *reinterpret_cast<const float2 *>(p.app_v + o);
+        const int pn = seq_len_of(b) - 1;
+        if (pn >= 0 && pn < p.max_pages * p.page_size) {
+            const int tn = pn / kTile;
+            if (tn >= tile_lo && tn < tile_hi && (tn - tile_lo) % kDecodeWaves == wave_u) {
+                t_new = tn;
+                r_new = pn - tn * kTile;
+            }
+        }
+    }
     __syncthreads();
     const half8 *qrow = reinterpret_cast<const half8 *>(lds_q) + (n % G) * (HD / 8) + hh;
 
@@ -278,6 +352,26 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
         // an invalid page id (tile_ok false) leaves the registers stale: the
         // tile then runs fully masked and contributes nothing
         const bool dead = !tile_ok;
+        if constexpr (APP) {
+            if (t == t_new) {
+                // the new token's rows through the wave's LDS: K dims 16c + 8hh
+                // of row r_new into the operand, V after the V tile below
+                _Float16 *nk = &lds_new[wave_u][0][0];
+                _Float16 *nv = &lds_new[wave_u][1][0];
+                if (lane < APL) {
+                    *reinterpret_cast<half2v *>(nk + app_e) = half2v{(_Float16)app_ok.x, (_Float16)app_ok.y};
+                    *reinterpret_cast<half2v *>(nv + app_e) = half2v{(_Float16)app_ov.x, (_Float16)app_ov.y};
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int c = 0; c < KC; ++c) {
+                    const half8 h = *reinterpret_cast<const half8 *>(nk + 16 * c + 8 * hh);
+                    kf[c] = n == r_new ? h : kf[c];
+                }
+            }
+        }
         // S^T = K * Q^T
         floatx16 s0 = floatx16{};
 #pragma unroll
@@ -299,6 +393,13 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
                 const bool ok = !dead && pos0 + r >= lo && pos0 + r < n_kv;
                 *reinterpret_cast<half8 *>(vt + r * VROW + 16 * (lane % CPR)) = ok ? vr[i] : half8{};
             }
+        }
+        if constexpr (APP) {
+            // row r_new of the V tile (after every lane's tile stores: a
+            // wave's LDS operations complete in order)
+            if (t == t_new && !dead && lane < CPR)
+                *reinterpret_cast<half8 *>(vt + r_new * VROW + 16 * lane) =
+                    *reinterpret_cast<const half8 *>(&lds_new[wave_u][1][8 * lane]);
         }
         // registers are free: start the next tile's loads now
         const bool next_ok = t + kDecodeWaves < tile_hi ? issue(t + kDecodeWaves, page_of(t + kDecodeWaves)) : false;
@@ -383,6 +484,7 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
     }
 
     l_run += xor32(l_run);
+    app_write();
     split_epilogue<HD, G>(o, m_run, l_run, lds_m, lds_l, lds_o, p, kvh, sp.rec0 + sp.split, sp.n_b, out_b,
                           wave, n, hh);
 }
@@ -2182,6 +2284,11 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
             }
         } else if (p.kv_type == SFA_KV_F32) {
             hipLaunchKernelGGL((decode_f32_kernel<HD, G>), grid, dim3(256), 0, s, p);
+        } else if (p.app_k != nullptr) {
+            if (B == 1)
+                hipLaunchKernelGGL((decode_f16_kernel<HD, G, true, true>), grid, dim3(256), 0, s, p);
+            else
+                hipLaunchKernelGGL((decode_f16_kernel<HD, G, false, true>), grid, dim3(256), 0, s, p);
         } else {
             if (B == 1)
                 hipLaunchKernelGGL((decode_f16_kernel<HD, G, true>), grid, dim3(256), 0, s, p);
@@ -2252,6 +2359,8 @@ int decode_setup(const sfa_kv_desc *kv, const float *q, float *out, const int32_
     p.scale_log2 = scale * 1.4426950408889634f;
     p.part = static_cast<float *>(workspace);
     p.kv_type = kv->kv_type;
+    p.app_k = p.app_v = nullptr;
+    p.app_k_pages = p.app_v_pages = p.app_k_cold = p.app_v_cold = nullptr;
     *out_p = p;
     return SFA_OK;
 }
@@ -2278,6 +2387,27 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
                                 workspace, ws_bytes, &p);
     if (rc != SFA_OK) return rc;
     return decode_run(p, kv->head_dim, passes, stream);
+}
+
+// Decode with each sequence's new token appended in the split pass (F16
+// caches): k, v [B][Hkv][head_dim] f32, token b at position seq_len[b] - 1.
+int decode_append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const float *q,
+                         float *out, const int32_t *page_table, int32_t max_pages,
+                         const int32_t *seq_len, const int32_t *kv_lo, int32_t B, int32_t max_seq_len,
+                         float scale, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    if (kv->kv_type != SFA_KV_F16) return SFA_ERR_UNSUPPORTED;
+    if (k == nullptr || v == nullptr) return SFA_ERR_INVALID_ARGUMENT;
+    DecodeParams p;
+    const int rc = decode_setup(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,
+                                workspace, ws_bytes, &p);
+    if (rc != SFA_OK) return rc;
+    p.app_k = k;
+    p.app_v = v;
+    p.app_k_pages = static_cast<uint8_t *>(kv->k_pages);
+    p.app_v_pages = static_cast<uint8_t *>(kv->v_pages);
+    p.app_k_cold = static_cast<uint8_t *>(kv->k_cold);
+    p.app_v_cold = static_cast<uint8_t *>(kv->v_cold);
+    return decode_run(p, kv->head_dim, 3, stream);
 }
 
 // ---- allocation-free decode ----------------------------------------------------

@@ -432,6 +432,25 @@ SFA_API int sfa_pager_attend(sfa_pager *p, int32_t layer, const float *q, float 
     return SFA_OK;
 }
 
+SFA_API int sfa_pager_append_attend(sfa_pager *p, int32_t layer, const float *k, const float *v,
+                                    const float *q, float *out, void *stream) {
+    if (p == nullptr || !p->step_open || layer < 0 || layer >= p->cfg.n_layer)
+        return SFA_ERR_INVALID_ARGUMENT;
+    const bool one_each = std::all_of(p->step_ntok.begin(), p->step_ntok.end(),
+                                      [](int32_t n) { return n == 1; });
+    if (!one_each || p->cfg.kv_type != SFA_KV_F16) {
+        const int rc = sfa_pager_append(p, layer, k, v, stream);
+        return rc != SFA_OK ? rc : sfa_pager_attend(p, layer, q, out, stream);
+    }
+    // one token per sequence, token b of sequence b at position seq_len[b] - 1
+    const sfa_kv_desc *d = &p->descs[layer];
+    const float scale = 1.0f / std::sqrt((float)p->cfg.head_dim);
+    const bool windowed = p->cfg.attend == SFA_ATTEND_WINDOW;
+    return sfa_attn_decode_append(d, k, v, q, out, p->d_table, p->max_pages, p->d_seq_len,
+                                  windowed ? p->d_kv_lo : nullptr, p->cfg.n_seq, p->max_span, scale,
+                                  p->ws, p->ws_bytes, stream);
+}
+
 SFA_API int sfa_pager_reset(sfa_pager *p, int32_t seq, void *stream) {
     if (p == nullptr || seq < 0 || seq >= p->cfg.n_seq) return SFA_ERR_INVALID_ARGUMENT;
     std::vector<sfa::PageAction> actions;

@@ -182,6 +182,30 @@ class PagedKV:
             _lib.check(lib.sfa_attn_decode_merge(*args), "sfa_attn_decode_merge")
         return out
 
+    def decode_append(self, layer: int, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
+                      page_table: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int,
+                      kv_lo: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                      scale: float | None = None, stream=None) -> torch.Tensor:
+        """Appends each sequence's new token (k, v [B, Hkv, hd] f32, token b at
+        position seq_len[b] - 1) and attends: out [B, Hq*hd] f32.  F16 pools."""
+        B = int(seq_len.numel())
+        assert q.is_contiguous() and q.dtype == torch.float32 and q.shape == (B, self.n_head, self.head_dim)
+        for t in (k, v):
+            assert t.is_contiguous() and t.dtype == torch.float32 and t.shape == (B, self.n_head_kv, self.head_dim)
+        assert page_table.dtype == torch.int32 and page_table.shape[0] == B
+        if out is None:
+            out = torch.empty((B, self.n_head * self.head_dim), dtype=torch.float32, device=q.device)
+        ws = self.workspace(B, max_seq_len)
+        lib = _lib.load()
+        _lib.check(lib.sfa_attn_decode_append(ctypes.byref(self._descs[layer]), k.data_ptr(), v.data_ptr(),
+                                              q.data_ptr(), out.data_ptr(), page_table.data_ptr(),
+                                              int(page_table.shape[1]), seq_len.data_ptr(), _ptr(kv_lo), B,
+                                              int(max_seq_len),
+                                              float(scale if scale is not None else self.scale),
+                                              ws.data_ptr(), ws.numel(), _stream(stream)),
+                   "sfa_attn_decode_append")
+        return out
+
     def prefill(self, layer: int, q: torch.Tensor, page_table: torch.Tensor, q_pos0: int,
                 kv_lo: int = 0, out: torch.Tensor | None = None, scale: float | None = None,
                 stream=None) -> torch.Tensor:

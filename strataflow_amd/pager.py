@@ -94,6 +94,22 @@ class KvPager:
                                                      _stream()), "sfa_pager_attend")
         return out
 
+    def append_attend(self, layer: int, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+        """append then attend in one call (fused for a one-token-per-sequence
+        step over an F16 cache)."""
+        assert k.is_contiguous() and v.is_contiguous() and k.dtype == torch.float32
+        assert k.shape == (self.n_tokens, self.n_head_kv, self.head_dim) and v.shape == k.shape
+        assert q.is_contiguous() and q.dtype == torch.float32
+        assert q.shape == (self.n_tokens, self.n_head, self.head_dim)
+        if out is None:
+            out = torch.empty((self.n_tokens, self.n_head * self.head_dim), dtype=torch.float32,
+                              device=q.device)
+        _lib.check(_lib.load_host().sfa_pager_append_attend(self._h, layer, k.data_ptr(), v.data_ptr(),
+                                                            q.data_ptr(), out.data_ptr(), _stream()),
+                   "sfa_pager_append_attend")
+        return out
+
     def reset(self, seq: int) -> None:
         _lib.check(_lib.load_host().sfa_pager_reset(self._h, seq, _stream()), "sfa_pager_reset")
 
