@@ -173,8 +173,8 @@ SFA_API int sfa_attn_decode(const sfa_kv_desc *kv, const float *q, float *out,
  * Equals sfa_kv_append(k, v, seq = b, pos = seq_len[b] - 1) followed by
  * sfa_attn_decode, bit for bit, pool bytes included (a position past the
  * table, or on a page id that is not there, is skipped as the append skips
- * it).  F16 caches only: SFA_ERR_UNSUPPORTED for F32 and Q8_0, whose callers
- * issue the two calls. */
+ * it).  F16 and F32 caches: SFA_ERR_UNSUPPORTED for Q8_0, whose callers issue
+ * the two calls. */
 SFA_API int sfa_attn_decode_append(const sfa_kv_desc *kv, const float *k, const float *v,
                                    const float *q, float *out, const int32_t *page_table,
                                    int32_t max_pages, const int32_t *seq_len, const int32_t *kv_lo,

@@ -109,7 +109,7 @@ SFA_API int sfa_pager_attend(sfa_pager *pager, int32_t layer, const float *q, fl
 
 /* sfa_pager_append then sfa_pager_attend for one layer, in one call: the
  * reference's attention node with its append (engine.cpp:1633-1762).  A step
- * with one token per sequence over an F16 cache runs them fused
+ * with one token per sequence over an F16 or F32 cache runs them fused
  * (sfa_attn_decode_append: one launch fewer, the same bytes and results);
  * other steps issue the two calls. */
 SFA_API int sfa_pager_append_attend(sfa_pager *pager, int32_t layer, const float *k, const float *v,

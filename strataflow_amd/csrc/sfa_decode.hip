@@ -504,8 +504,9 @@ __global__ __launch_bounds__(256, 2) void decode_f16_kernel(DecodeParams p) {
 // per instruction, no registers) with the 16-byte chunks of row r XORed by
 // 4 * ((r / 4) % 4), so the four quarters' V^T reads (rows 4 apart) fall in
 // different LDS banks.  At 4 bytes per element the kernel stays bound by HBM
-// at long contexts.
-template <int HD, int G>
+// at long contexts.  APP: the fused append, as in decode_f16_kernel (rows
+// stored as f32, as the append stores them).
+template <int HD, int G, bool APP = false>
 __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeParams p) {
     static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim");
     static_assert(G >= 1 && G <= 16 && (16 % G) == 0, "group size");
@@ -524,6 +525,8 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     __shared__ float lds_l[kDecodeWaves][G];
     __shared__ __attribute__((aligned(16))) float lds_q[G * HD];
     __shared__ float lds_o[kDecodeWaves][G][HD];
+    // APP: the owner wave's new K row, staged for its operand
+    __shared__ __attribute__((aligned(16))) float lds_newk[APP ? kDecodeWaves : 1][APP ? HD : 4];
 
     const int kvh = (int)blockIdx.x / p.split_row;
     const int slot = (int)blockIdx.x - kvh * p.split_row;
@@ -599,12 +602,52 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     bool v_pending = tile_ok;  // the guessed tile's V loads are in flight into vt
     issue_v();
 
+    // APP writer (wave 0 of slot j < B writes sequence j's new row): two
+    // elements per lane, loaded behind the first tile
+    constexpr int APL = HD / 2;
+    const int app_e = 2 * (lane < APL ? lane : APL - 1);
+    const int app_ws = slot < p.n_seq ? slot : p.n_seq - 1;
+    float2 app_wk{}, app_wv{};
+    if constexpr (APP) {
+        const int64_t o = ((int64_t)app_ws * Hkv + kvh) * HD + app_e;
+        app_wk = *reinterpret_cast<const float2 *>(p.app_k + o);
+        app_wv = *reinterpret_cast<const float2 *>(p.app_v + o);
+    }
+
     SlotPlan sp;
-    if (!plan(p, raw, slot, -1, lane, sp)) {
+    const bool active = plan(p, raw, slot, -1, lane, sp);
+    // raw seq_len of sequence j: lane j of the plan's loads (up to 64 sequences)
+    auto seq_len_of = [&](int j) -> int {
+        return p.n_seq <= kWave ? __builtin_amdgcn_readlane(raw.n_kv, j) : p.seq_len[j];
+    };
+    int app_pn = -1;
+    int32_t app_wid = -1;
+    if constexpr (APP) {
+        const int pn = seq_len_of(app_ws) - 1;
+        const int lp = pn < 0 ? 0 : pn / p.page_size;
+        app_pn = slot < p.n_seq && wave_u == 0 && pn >= 0 && lp < p.max_pages ? pn : -1;
+        app_wid = p.page_table[(int64_t)app_ws * p.max_pages + (lp < p.max_pages ? lp : p.max_pages - 1)];
+    }
+    auto app_write = [&]() {
+        if constexpr (APP) {
+            if (app_pn < 0) return;
+            uint8_t *kb = const_cast<uint8_t *>(
+                page_base(app_wid, p.app_k_pages, p.n_pages, p.app_k_cold, p.n_cold, p.page_bytes));
+            uint8_t *vb = const_cast<uint8_t *>(
+                page_base(app_wid, p.app_v_pages, p.n_pages, p.app_v_cold, p.n_cold, p.page_bytes));
+            if (kb == nullptr || vb == nullptr || lane >= APL) return;
+            const int lp = app_pn / p.page_size;
+            const int64_t off = ((int64_t)(app_pn - lp * p.page_size) * Hkv + kvh) * p.row_bytes + 4 * app_e;
+            *reinterpret_cast<float2 *>(kb + off) = app_wk;
+            *reinterpret_cast<float2 *>(vb + off) = app_wv;
+        }
+    };
+    if (!active) {
         if (p.n_seq == 1 && slot == 0 && sp.n_b == 0) {
             float *out0 = p.out + (int64_t)kvh * G * HD;
             for (int i = threadIdx.x; i < G * HD; i += blockDim.x) out0[i] = 0.0f;
         }
+        app_write();
         // the wave's LDS loads must land before the workgroup ends
         __builtin_amdgcn_s_waitcnt(0);
         return;
@@ -637,6 +680,22 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
         }
         issue_v();
     }
+    // APP owner: the wave whose tiles include sequence b's new position
+    int t_new = -1, r_new = 0;
+    float2 app_ok{}, app_ov{};
+    if constexpr (APP) {
+        const int64_t o = ((int64_t)b * Hkv + kvh) * HD + app_e;
+        app_ok = *reinterpret_cast<const float2 *>(p.app_k + o);
+        app_ov = *reinterpret_cast<const float2 *>(p.app_v + o);
+        const int pn = seq_len_of(b) - 1;
+        if (pn >= 0 && pn < p.max_pages * p.page_size) {
+            const int tn = pn / kTile;
+            if (tn >= tile_lo && tn < tile_hi && (tn - tile_lo) % kDecodeWaves == wave_u) {
+                t_new = tn;
+                r_new = pn - tn * kTile;
+            }
+        }
+    }
     __syncthreads();
     const float *qcol = lds_q + (c16 % G) * HD + QD * qt;
 
@@ -650,6 +709,25 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
     for (; t < tile_hi; t += kDecodeWaves) {
         const int pos0 = t * kTile;
         const bool dead = !tile_ok;
+        if constexpr (APP) {
+            if (t == t_new) {
+                // the new K row through the wave's LDS into the operand of
+                // lanes c16 == r_new % 16, row block r_new / 16
+                if (lane < APL) *reinterpret_cast<float2 *>(&lds_newk[wave_u][app_e]) = app_ok;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const bool mine = c16 == (r_new & 15);
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+                    for (int j = 0; j < KQ4; ++j) {
+                        const floatx4 nk = *reinterpret_cast<const floatx4 *>(&lds_newk[wave_u][QD * qt + 4 * j]);
+                        kf[rb][j] = (mine && rb == (r_new >> 4)) ? nk : kf[rb][j];
+                    }
+                }
+            }
+        }
         // S^T = K * Q^T: row block rb, k step 4j + e is dim QD*qt + 4j + e
         floatx4 s[2] = {floatx4{}, floatx4{}};
 #pragma unroll
@@ -710,6 +788,17 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KV4) : "memory");
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if constexpr (APP) {
+            // row r_new of the landed V tile (logical chunk c at chunk c ^ the
+            // row's swizzle), before any lane reads it
+            if (t == t_new && !dead && lane < APL) {
+                const int sw = (4 * ((r_new >> 2) & 3)) & (CPR - 1);
+                *reinterpret_cast<float2 *>(vt + r_new * VRB + 16 * ((lane >> 1) ^ sw) + 8 * (lane & 1)) = app_ov;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int r = 16 * (i >> 2) + 4 * qt + (i & 3);
@@ -730,6 +819,7 @@ __global__ __launch_bounds__(256, G <= 4 ? 2 : 1) void decode_f32_kernel(DecodeP
         tile_ok = next_ok;
     }
     __builtin_amdgcn_s_waitcnt(0);
+    app_write();
 
     // the column's sum over the four quarters; one replica of each head
     // (columns c16 < g) stages its (m, l, O^T): register r of block d is dim
@@ -2283,7 +2373,10 @@ static void launch_f16(const DecodeParams &p, int B, int Hkv, int passes, hipStr
                     hipLaunchKernelGGL((decode_q8_kernel<HD, G, false, false>), grid, dim3(256), 0, s, p);
             }
         } else if (p.kv_type == SFA_KV_F32) {
-            hipLaunchKernelGGL((decode_f32_kernel<HD, G>), grid, dim3(256), 0, s, p);
+            if (p.app_k != nullptr)
+                hipLaunchKernelGGL((decode_f32_kernel<HD, G, true>), grid, dim3(256), 0, s, p);
+            else
+                hipLaunchKernelGGL((decode_f32_kernel<HD, G>), grid, dim3(256), 0, s, p);
         } else if (p.app_k != nullptr) {
             if (B == 1)
                 hipLaunchKernelGGL((decode_f16_kernel<HD, G, true, true>), grid, dim3(256), 0, s, p);
@@ -2389,13 +2482,13 @@ int decode_launch(const sfa_kv_desc *kv, const float *q, float *out, const int32
     return decode_run(p, kv->head_dim, passes, stream);
 }
 
-// Decode with each sequence's new token appended in the split pass (F16
-// caches): k, v [B][Hkv][head_dim] f32, token b at position seq_len[b] - 1.
+// Decode with each sequence's new token appended in the split pass (F16 and
+// F32 caches): k, v [B][Hkv][head_dim] f32, token b at position seq_len[b] - 1.
 int decode_append_launch(const sfa_kv_desc *kv, const float *k, const float *v, const float *q,
                          float *out, const int32_t *page_table, int32_t max_pages,
                          const int32_t *seq_len, const int32_t *kv_lo, int32_t B, int32_t max_seq_len,
                          float scale, void *workspace, size_t ws_bytes, hipStream_t stream) {
-    if (kv->kv_type != SFA_KV_F16) return SFA_ERR_UNSUPPORTED;
+    if (kv->kv_type != SFA_KV_F16 && kv->kv_type != SFA_KV_F32) return SFA_ERR_UNSUPPORTED;
     if (k == nullptr || v == nullptr) return SFA_ERR_INVALID_ARGUMENT;
     DecodeParams p;
     const int rc = decode_setup(kv, q, out, page_table, max_pages, seq_len, kv_lo, B, max_seq_len, scale,

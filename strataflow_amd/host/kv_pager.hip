@@ -438,7 +438,7 @@ SFA_API int sfa_pager_append_attend(sfa_pager *p, int32_t layer, const float *k,
         return SFA_ERR_INVALID_ARGUMENT;
     const bool one_each = std::all_of(p->step_ntok.begin(), p->step_ntok.end(),
                                       [](int32_t n) { return n == 1; });
-    if (!one_each || p->cfg.kv_type != SFA_KV_F16) {
+    if (!one_each || p->cfg.kv_type == SFA_KV_Q8_0) {
         const int rc = sfa_pager_append(p, layer, k, v, stream);
         return rc != SFA_OK ? rc : sfa_pager_attend(p, layer, q, out, stream);
     }

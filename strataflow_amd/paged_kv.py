@@ -187,7 +187,7 @@ class PagedKV:
                       kv_lo: torch.Tensor | None = None, out: torch.Tensor | None = None,
                       scale: float | None = None, stream=None) -> torch.Tensor:
         """Appends each sequence's new token (k, v [B, Hkv, hd] f32, token b at
-        position seq_len[b] - 1) and attends: out [B, Hq*hd] f32.  F16 pools."""
+        position seq_len[b] - 1) and attends: out [B, Hq*hd] f32.  F16 or F32 pools."""
         B = int(seq_len.numel())
         assert q.is_contiguous() and q.dtype == torch.float32 and q.shape == (B, self.n_head, self.head_dim)
         for t in (k, v):

@@ -97,7 +97,7 @@ class KvPager:
     def append_attend(self, layer: int, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
                       out: torch.Tensor | None = None) -> torch.Tensor:
         """append then attend in one call (fused for a one-token-per-sequence
-        step over an F16 cache)."""
+        step over an F16 or F32 cache)."""
         assert k.is_contiguous() and v.is_contiguous() and k.dtype == torch.float32
         assert k.shape == (self.n_tokens, self.n_head_kv, self.head_dim) and v.shape == k.shape
         assert q.is_contiguous() and q.dtype == torch.float32

@@ -41,15 +41,16 @@ def _assert_same(c, out0, out1, what):
     assert torch.equal(c.dev.v[0], c.dev.v[1]), f"{what}: V pools differ"
 
 
+@pytest.mark.parametrize("kv_type", [1, 0])
 @pytest.mark.parametrize("shape", [(32, 8, 128), (8, 2, 64), (8, 4, 32), (16, 16, 128)])
 @pytest.mark.parametrize("n_kv,page_size", [(1, 256), (33, 32), (256, 256), (257, 256), (4096, 256),
                                             (3001, 64)])
-def test_decode_append_one_sequence(gpu, oracle_mod, shape, n_kv, page_size):
+def test_decode_append_one_sequence(gpu, oracle_mod, kv_type, shape, n_kv, page_size):
     # the new token on the first position, a tile's first row, a page's last
-    # and first rows, at ctx 4096
+    # and first rows, at ctx 4096; F16 and F32 caches
     Hq, Hkv, hd = shape
     c = Case(oracle_mod, seq_lens=[n_kv], n_head=Hq, n_head_kv=Hkv, head_dim=hd, page_size=page_size,
-             seed=n_kv + hd, n_layer=2)
+             seed=n_kv + hd, n_layer=2, kv_type=kv_type)
     k, v = _new_tokens(gpu, 1, Hkv, hd, n_kv + 1)
     out0, out1 = _unfused_vs_fused(c, k, v, n_kv)
     _assert_same(c, out0, out1, f"{shape} n_kv={n_kv}")
@@ -60,29 +61,32 @@ def test_decode_append_one_sequence(gpu, oracle_mod, shape, n_kv, page_size):
     ([100, 50, 33], [0, 60, 32]),                      # seq_len <= kv_lo: nothing attended, row written
     ([4097, 4000, 129, 2], None),                      # the window leg's shape, lossless
 ])
-def test_decode_append_batches(gpu, oracle_mod, seq, lo):
-    c = Case(oracle_mod, seq_lens=seq, kv_lo=lo, seed=len(seq) * 7, n_layer=2)
+@pytest.mark.parametrize("kv_type", [1, 0])
+def test_decode_append_batches(gpu, oracle_mod, seq, lo, kv_type):
+    c = Case(oracle_mod, seq_lens=seq, kv_lo=lo, seed=len(seq) * 7, n_layer=2, kv_type=kv_type)
     k, v = _new_tokens(gpu, c.B, c.n_head_kv, c.head_dim, 5)
     out0, out1 = _unfused_vs_fused(c, k, v, max(seq))
     _assert_same(c, out0, out1, f"seq {seq} lo {lo}")
 
 
-def test_decode_append_batch_over_64(gpu, oracle_mod):
+@pytest.mark.parametrize("kv_type", [1, 0])
+def test_decode_append_batch_over_64(gpu, oracle_mod, kv_type):
     # more sequences than a wave has lanes: the kernel reads seq_len per sequence
     rng = np.random.default_rng(70)
     seq = rng.integers(1, 600, 70)
     c = Case(oracle_mod, seq_lens=seq, n_head=8, n_head_kv=2, head_dim=64, page_size=64, seed=70,
-             n_layer=2)
+             n_layer=2, kv_type=kv_type)
     k, v = _new_tokens(gpu, c.B, c.n_head_kv, c.head_dim, 71)
     out0, out1 = _unfused_vs_fused(c, k, v, int(seq.max()))
     _assert_same(c, out0, out1, "B=70")
 
 
-def test_decode_append_missing_page(gpu, oracle_mod):
+@pytest.mark.parametrize("kv_type", [1, 0])
+def test_decode_append_missing_page(gpu, oracle_mod, kv_type):
     # the new token's page id is -1 for sequence 1: the append skips it and
     # its tile is masked, in both forms
     import torch
-    c = Case(oracle_mod, seq_lens=[500, 300, 40], seed=3, n_layer=2, page_size=64)
+    c = Case(oracle_mod, seq_lens=[500, 300, 40], seed=3, n_layer=2, page_size=64, kv_type=kv_type)
     lp = (300 - 1) // 64
     c.page_table[1, lp] = -1
     c.t_pt = torch.from_numpy(c.page_table).to(gpu)
@@ -103,17 +107,19 @@ def test_decode_append_matches_oracle(gpu, oracle_mod):
     assert_close(out1.cpu().numpy(), c.oracle(oracle_mod.GGML), what="fused vs ggml")
 
 
-def test_decode_append_cold_page(gpu):
+@pytest.mark.parametrize("kv_type", [1, 0])
+def test_decode_append_cold_page(gpu, kv_type):
     # the new position on a cold page (id -2): written to the host-pinned pool
     import torch
     from strataflow_amd.paged_kv import PagedKV
     Hq, Hkv, hd, ps = 16, 4, 128, 32
-    kv = PagedKV(2, Hq, Hkv, hd, 1, ps, 4, device=gpu, n_cold_pages=2)
+    kv = PagedKV(2, Hq, Hkv, hd, kv_type, ps, 4, device=gpu, n_cold_pages=2)
     g = torch.Generator(device="cpu")
     g.manual_seed(9)
-    # the same f16 values (normal, |x| < 2) in both layers' device and cold pools
+    # the same values (|x| < 2) in both layers' device and cold pools
+    dt, es = (torch.float16, 2) if kv_type == 1 else (torch.float32, 4)
     for pool in (kv.k, kv.v, kv.k_cold, kv.v_cold):
-        vals = (torch.rand(pool[0].numel() // 2, generator=g) * 4 - 2).to(torch.float16)
+        vals = (torch.rand(pool[0].numel() // es, generator=g) * 4 - 2).to(dt)
         pool.copy_(vals.view(torch.uint8).view(pool[0].shape).expand_as(pool))
     pt = torch.tensor([[0, -2, 1]], dtype=torch.int32, device=gpu)  # positions 32..63 cold page 0
     sl = torch.tensor([45], dtype=torch.int32, device=gpu)
@@ -128,8 +134,8 @@ def test_decode_append_cold_page(gpu):
     assert torch.equal(kv.k[0], kv.k[1]) and torch.equal(kv.v[0], kv.v[1])
 
 
-@pytest.mark.parametrize("kv_type", [0, 8])
-def test_decode_append_refuses_f32_and_q8(gpu, oracle_mod, kv_type):
+@pytest.mark.parametrize("kv_type", [8])
+def test_decode_append_refuses_q8(gpu, oracle_mod, kv_type):
     from strataflow_amd import _lib
     c = Case(oracle_mod, seq_lens=[100], kv_type=kv_type, seed=1, n_layer=1)
     k, v = _new_tokens(gpu, 1, c.n_head_kv, c.head_dim, 2)
@@ -138,16 +144,19 @@ def test_decode_append_refuses_f32_and_q8(gpu, oracle_mod, kv_type):
     assert e.value.status == _lib.SFA_ERR_UNSUPPORTED
 
 
+@pytest.mark.parametrize("kv_type", ["f16", "f32", "q8_0"])
 @pytest.mark.parametrize("attend", ["window", "lossless"])
-def test_pager_append_attend_equals_two_calls(gpu, attend):
+def test_pager_append_attend_equals_two_calls(gpu, attend, kv_type):
     # two pagers with the same placement: append + attend against the fused
     # call over decode steps that cross pages and evict (a wrong row written at
     # one step shows in the next steps' outputs)
     import torch
-    from strataflow_amd.pager import SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, KvPager
+    from strataflow_amd.pager import (SFA_ATTEND_LOSSLESS, SFA_ATTEND_WINDOW, SFA_KV_F16, SFA_KV_F32,
+                                      SFA_KV_Q8_0, KvPager)
     B, Hq, Hkv, hd, ps = 3, 16, 4, 128, 64
     mode = SFA_ATTEND_WINDOW if attend == "window" else SFA_ATTEND_LOSSLESS
-    mk = lambda: KvPager(n_layer=1, n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=SFA_KV_F16,
+    kvt = {"f16": SFA_KV_F16, "f32": SFA_KV_F32, "q8_0": SFA_KV_Q8_0}[kv_type]  # Q8_0: the two calls
+    mk = lambda: KvPager(n_layer=1, n_head=Hq, n_head_kv=Hkv, head_dim=hd, kv_type=kvt,
                          page_size=ps, n_seq=B, n_ctx=1024, window=256, attend=mode, seed=5)
     pa, pb = mk(), mk()
     g = torch.Generator(device=gpu)
