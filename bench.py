@@ -1126,6 +1126,11 @@ def main():
                 pf[f"{prefix}_us_per_layer_chunk"] = leg.get("us_per_layer_chunk")
                 pf[f"{prefix}_frac"] = leg.get("frac")
     result["legs"] = legs_summary(result)
+    # every leg's figures also as scalar fields of the headline's roofline
+    # object (a record that keeps only the contract's objects keeps them)
+    for k, v in result["legs"].items():
+        if not k.startswith("decode_f16_4k"):
+            roof[k] = v
     print(json.dumps(result))
 
 
