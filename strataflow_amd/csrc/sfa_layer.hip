@@ -29,10 +29,9 @@
 
 namespace sfa {
 
-// expert gate/up rows per wave (one gate and one up row): the waves stay
-// small enough for eight per SIMD and Mixtral's 2 x 14336 rows per slot fill
-// the chip in one pass (79 us for two experts' 470 MB; 2 / 4 / 8 rows per
-// wave: 81 / 89 / 104 us)
+// expert gate/up rows per wave (one gate and one up row): Mixtral's 2 x 14336
+// rows per slot give 28672 waves (2 / 4 / 8 rows per wave were slower: 81 /
+// 89 / 104 us against 79 for two experts' 470 MB)
 constexpr int kRowsPerWave = 1;
 constexpr int kLayerWaves = 4;
 constexpr int kRowsPerBlock = kRowsPerWave * kLayerWaves;  // expert gate/up rows per workgroup
@@ -140,8 +139,11 @@ struct GemvParams {
 // Wave w of block b owns rows RW * (4b + w) .. + RW - 1 (clamped to n_out - 1
 // for the loads, not stored) for NT tokens starting at token blockIdx.y * NT.
 // RW follows n_out so that a launch has about 4096 waves or more: one row per
-// wave for the 4096- and 6144-row products of a decode layer (every chunk of
-// a row in flight at once), four for wide ones.
+// wave for the 4096- and 6144-row products of a decode layer, four for wide
+// ones.  One token's F16 row loads kGemvBatch chunks a lane (activations and
+// weights) before it uses any: a load-use loop holds fewer in flight
+// (`wo` 4096 x 4096 and the Q/K/V stack, layer 165.3 -> 163.2 us).
+constexpr int kGemvBatch = 4;
 template <bool F16, int NT, int RW>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const int lane = threadIdx.x & 63;
@@ -161,9 +163,32 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) toks[t] = min(tok0 + t, p.n_rows - 1);
 
+    int c_rest = lane;
+    if constexpr (F16 && RW == 1 && NT == 1) {
+        // one token's row (the decode case): whole batches of kGemvBatch
+        // chunks a lane, activations then weights, loaded before any is used
+        const half8 *W = static_cast<const half8 *>(p.w);
+        const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)toks[0] * p.n_in);
+        constexpr int CB = kGemvBatch;
+        const int full = nc / (64 * CB) * (64 * CB);
+        for (int c0 = lane; c0 < full; c0 += 64 * CB) {
+            half8 wv[CB];
+            floatx4 x0[CB], x1[CB];
+#pragma unroll
+            for (int k = 0; k < CB; ++k) {
+                x0[k] = xr[2 * (c0 + 64 * k)];
+                x1[k] = xr[2 * (c0 + 64 * k) + 1];
+            }
+#pragma unroll
+            for (int k = 0; k < CB; ++k) wv[k] = W[(int64_t)rows[0] * nc + c0 + 64 * k];
+#pragma unroll
+            for (int k = 0; k < CB; ++k) acc[0][0] = dot8(wv[k], to_half8(x0[k], x1[k]), acc[0][0]);
+        }
+        c_rest = full + lane;
+    }
     constexpr int kUnroll = RW == 1 ? 8 : 4;
 #pragma unroll kUnroll
-    for (int c = lane; c < nc; c += 64) {
+    for (int c = c_rest; c < nc; c += 64) {
         if constexpr (F16) {
             const half8 *W = static_cast<const half8 *>(p.w);
             half8 wv[RW];
@@ -340,11 +365,17 @@ struct MoeParams {
     int n_rows, n_embd, n_ff, n_expert, n_used;
 };
 
+// chunks of 8 a lane loads before it uses any in the F16 gate/up product;
+// the F16 kernel is built for four waves per SIMD so that the compiler keeps
+// them all in flight (the launch has 28672 waves for Mixtral's two slots, so
+// the chip stays full)
+constexpr int kGateUpBatch = 8;
+
 // act[t][j][f] = silu(gate[e][f] . x[t]) * (up[e][f] . x[t]), e = ids[t][j];
 // an id outside [0, n_expert) gives zeros.  Grid (row blocks of n_ff, n_used,
 // n_rows).
 template <bool F16>
-__global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, F16 ? 4 : 8))) void moe_gate_up_kernel(MoeParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int f0 = (int)blockIdx.x * kRowsPerBlock + wave * kRowsPerWave;
@@ -362,8 +393,38 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeParams p) {
     }
     const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)t * p.n_embd);
     const int64_t mat = (int64_t)e * p.n_ff;
+    int c_rest = lane;
+    if constexpr (F16 && kRowsPerWave == 1) {
+        // whole batches of kGateUpBatch chunks a lane: the activations, then
+        // the gate and up rows, all loaded before any is used (a whole
+        // 4096-wide row at once), then the products in chunk order
+        const half8 *G = static_cast<const half8 *>(p.gate), *U = static_cast<const half8 *>(p.up);
+        constexpr int CB = kGateUpBatch;
+        const int full = nc / (64 * CB) * (64 * CB);
+        for (int c0 = lane; c0 < full; c0 += 64 * CB) {
+            half8 gv[CB], uv[CB];
+            floatx4 x0[CB], x1[CB];
+#pragma unroll
+            for (int k = 0; k < CB; ++k) {
+                x0[k] = xr[2 * (c0 + 64 * k)];
+                x1[k] = xr[2 * (c0 + 64 * k) + 1];
+            }
+#pragma unroll
+            for (int k = 0; k < CB; ++k) {
+                gv[k] = G[(mat + rows[0]) * nc + c0 + 64 * k];
+                uv[k] = U[(mat + rows[0]) * nc + c0 + 64 * k];
+            }
+#pragma unroll
+            for (int k = 0; k < CB; ++k) {
+                const half8 xh = to_half8(x0[k], x1[k]);
+                g[0] = dot8(gv[k], xh, g[0]);
+                u[0] = dot8(uv[k], xh, u[0]);
+            }
+        }
+        c_rest = full + lane;
+    }
 #pragma unroll 4
-    for (int c = lane; c < nc; c += 64) {
+    for (int c = c_rest; c < nc; c += 64) {
         if constexpr (F16) {
             const half8 *G = static_cast<const half8 *>(p.gate), *U = static_cast<const half8 *>(p.up);
             half8 gv[kRowsPerWave], uv[kRowsPerWave];
@@ -414,13 +475,16 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeParams p) {
 
 // y[t][o] = (sum over slots j in order of (down[e_j][o] . act[t][j]) * w[t][j])
 // + residual[t][o]; a slot with an id outside [0, n_expert) adds nothing.
-// Every slot's rows stream in the same loop (NU slots, their loads in flight
-// together, four chunks ahead); two rows per wave, so a 4096-row output has
-// 2048 waves.  For F16 weights the activations arrive as halves.  Grid (row
-// blocks of n_embd, n_rows).
+// Every slot's rows stream in the same loop; two rows per wave, so a 4096-row
+// output has 2048 waves.  For F16 weights the activations arrive as halves,
+// and each lane loads kDownBatch 16-byte pieces (a batch of chunks of every
+// slot's two rows and activations) before it uses any; that kernel is built
+// for the two waves per SIMD such a launch has, so the compiler keeps the
+// batch in flight.  Grid (row blocks of n_embd, n_rows).
 constexpr int kDownRows = 2;
+constexpr int kDownBatch = 24;
 template <bool F16, int NU>
-__global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, F16 ? 2 : 8))) void moe_down_kernel(MoeParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int o0 = ((int)blockIdx.x * kLayerWaves + wave) * kDownRows;
@@ -447,21 +511,48 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeParams p) {
     for (int j = 0; j < NU; ++j)
 #pragma unroll
         for (int r = 0; r < kDownRows; ++r) d[j][r] = 0.0f;
+    if constexpr (F16) {
+        // CB chunks of every slot's rows and activations loaded before any is
+        // used: 2048 waves are eight a CU, so each keeps a whole batch in
+        // flight, not the six loads the compiler holds in a load-use loop.
+        // Whole batches first (no lane-dependent test the loads could sink
+        // into), then the chunks left, one at a time: products in chunk order.
+        const half8 *D = static_cast<const half8 *>(p.down);
+        constexpr int CB = kDownBatch / (NU * kDownRows + NU) > 0 ? kDownBatch / (NU * kDownRows + NU) : 1;
+        const int full = nc / (64 * CB) * (64 * CB);
+        auto chunk = [&](int c, half8 (&dv)[NU][kDownRows], half8 (&ah)[NU]) {
+#pragma unroll
+            for (int j = 0; j < NU; ++j) {
+#pragma unroll
+                for (int r = 0; r < kDownRows; ++r) dv[j][r] = D[(mat[j] + rows[r]) * nc + c];
+                ah[j] = act_h[(int64_t)j * nc + c];
+            }
+        };
+        auto use = [&](const half8 (&dv)[NU][kDownRows], const half8 (&ah)[NU]) {
+#pragma unroll
+            for (int j = 0; j < NU; ++j)
+#pragma unroll
+                for (int r = 0; r < kDownRows; ++r) d[j][r] = dot8(dv[j][r], ah[j], d[j][r]);
+        };
+        for (int c0 = lane; c0 < full; c0 += 64 * CB) {
+            half8 dv[CB][NU][kDownRows], ah[CB][NU];
+#pragma unroll
+            for (int k = 0; k < CB; ++k) chunk(c0 + 64 * k, dv[k], ah[k]);
+#pragma unroll
+            for (int k = 0; k < CB; ++k) use(dv[k], ah[k]);
+        }
+        for (int c = full + lane; c < nc; c += 64) {
+            half8 dv[NU][kDownRows], ah[NU];
+            chunk(c, dv, ah);
+            use(dv, ah);
+        }
+    } else {
+        const floatx4 *D = static_cast<const floatx4 *>(p.down);
 #pragma unroll 4
-    for (int c = lane; c < nc; c += 64) {
+        for (int c = lane; c < nc; c += 64) {
 #pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const floatx4 *ar = act + (int64_t)j * (p.n_ff / 4);
-            if constexpr (F16) {
-                const half8 *D = static_cast<const half8 *>(p.down);
-                half8 dv[kDownRows];
-#pragma unroll
-                for (int r = 0; r < kDownRows; ++r) dv[r] = D[(mat[j] + rows[r]) * nc + c];
-                const half8 ah = act_h[(int64_t)j * nc + c];
-#pragma unroll
-                for (int r = 0; r < kDownRows; ++r) d[j][r] = dot8(dv[r], ah, d[j][r]);
-            } else {
-                const floatx4 *D = static_cast<const floatx4 *>(p.down);
+            for (int j = 0; j < NU; ++j) {
+                const floatx4 *ar = act + (int64_t)j * (p.n_ff / 4);
                 floatx4 d0[kDownRows], d1[kDownRows];
 #pragma unroll
                 for (int r = 0; r < kDownRows; ++r) {
@@ -541,8 +632,28 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_rope_append_kernel(QkvRopePar
         const int nc = p.n_in / 8;
         const floatx4 *xr = reinterpret_cast<const floatx4 *>(p.x + (int64_t)tok * p.n_in);
         float acc = 0.0f;
+        int c_rest = lane;
+        if constexpr (F16) {  // gemv_kernel's batches for one token
+            const half8 *W = static_cast<const half8 *>(p.w);
+            constexpr int CB = kGemvBatch;
+            const int full = nc / (64 * CB) * (64 * CB);
+            for (int c0 = lane; c0 < full; c0 += 64 * CB) {
+                half8 wv[CB];
+                floatx4 x0[CB], x1[CB];
+#pragma unroll
+                for (int k = 0; k < CB; ++k) {
+                    x0[k] = xr[2 * (c0 + 64 * k)];
+                    x1[k] = xr[2 * (c0 + 64 * k) + 1];
+                }
+#pragma unroll
+                for (int k = 0; k < CB; ++k) wv[k] = W[(int64_t)row * nc + c0 + 64 * k];
+#pragma unroll
+                for (int k = 0; k < CB; ++k) acc = dot8(wv[k], to_half8(x0[k], x1[k]), acc);
+            }
+            c_rest = full + lane;
+        }
 #pragma unroll 8
-        for (int c = lane; c < nc; c += 64) {
+        for (int c = c_rest; c < nc; c += 64) {
             if constexpr (F16) {
                 const half8 *W = static_cast<const half8 *>(p.w);
                 acc = dot8(W[(int64_t)row * nc + c], to_half8(xr[2 * c], xr[2 * c + 1]), acc);
