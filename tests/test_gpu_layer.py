@@ -62,7 +62,8 @@ def test_rms_norm(gpu, n_rows, n):
 
 @pytest.mark.parametrize("wdtype", ["f32", "f16"])
 @pytest.mark.parametrize("n_rows,n_in,n_out", [(1, 256, 512), (1, 4096, 1000), (3, 512, 8),
-                                               (8, 256, 4096), (13, 1024, 256), (1, 14336, 64)])
+                                               (8, 256, 4096), (13, 1024, 256), (1, 14336, 64),
+                                               (1, 2056, 300)])  # whole load batches + one chunk more
 def test_mul_mat_vec(gpu, wdtype, n_rows, n_in, n_out):
     import torch
     from strataflow_amd import layer
@@ -150,7 +151,8 @@ def _moe_ref(x, res, ids, wts, g, u, d, f16):
 
 @pytest.mark.parametrize("wdtype", ["f32", "f16"])
 @pytest.mark.parametrize("n_rows,n_embd,n_ff,n_expert,k", [(1, 256, 512, 8, 2), (3, 512, 1024, 8, 2),
-                                                            (2, 4096, 1024, 4, 4), (1, 128, 2048, 16, 1)])
+                                                            (2, 4096, 1024, 4, 4), (1, 128, 2048, 16, 1),
+                                                            (1, 4160, 2560, 8, 2)])  # batches + chunks left
 def test_moe_ffn(gpu, wdtype, n_rows, n_embd, n_ff, n_expert, k):
     from strataflow_amd import layer
     rng = np.random.default_rng(n_embd + n_ff + k)

@@ -182,7 +182,8 @@ def test_rope_append_rejects_bad_arguments(gpu):
 
 @pytest.mark.parametrize("kv_type", [F32, F16])
 @pytest.mark.parametrize("wdtype", ["f32", "f16"])
-@pytest.mark.parametrize("shape,n_embd", [((32, 8, 128), 4096), ((8, 4, 32), 256), ((16, 8, 64), 512)])
+@pytest.mark.parametrize("shape,n_embd", [((32, 8, 128), 4096), ((8, 4, 32), 256), ((16, 8, 64), 512),
+                                          ((8, 2, 64), 2056)])
 def test_qkv_rope_append_equals_product_then_rope_append(gpu, kv_type, wdtype, shape, n_embd):
     """sfa_qkv_rope_kv_append gives the bits of sfa_mul_mat_vec followed by
     sfa_rope_kv_append on its Q, K and V parts: the rotated Q and every byte of
