@@ -1,5 +1,5 @@
-"""HIP-graph capture of the decode node and of a pager step, replayed with
-changing inputs.
+"""HIP-graph capture of the decode node and of a pager step (append + attend,
+or the two in one call), replayed with changing inputs.
 
 A captured decode is valid across steps only because every launch argument
 stays fixed: q, seq_len, kv_lo and the page table are device buffers the
@@ -131,12 +131,14 @@ def test_decode_32_layer_step_graph_replay(gpu, oracle_mod):
         assert torch.equal(out.view(torch.int32), eager.view(torch.int32)), f"seq_len {n}"
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("attend", [0, 1])
-def test_pager_step_graph_replay(gpu, attend):
+def test_pager_step_graph_replay(gpu, attend, fused):
     # two pagers fed the same stream: one runs every step eagerly, the other
-    # replays one captured step (append + attend of every layer) over fixed
-    # input buffers after its host-side begin(); pages are evicted (lossless)
-    # or released (window) during the replayed steps
+    # replays one captured step (append + attend of every layer, or the fused
+    # append_attend) over fixed input buffers after its host-side begin();
+    # pages are evicted (lossless) or released (window) during the replayed
+    # steps
     import torch
     from strataflow_amd import synth
     from strataflow_amd.pager import KvPager
@@ -168,6 +170,13 @@ def test_pager_step_graph_replay(gpu, attend):
             p.append(layer, k[layer], v[layer])
             p.attend(layer, q[layer], out[layer])
 
+    def layers_g(p, q, k, v, out):
+        if not fused:
+            layers(p, q, k, v, out)
+            return
+        for layer in range(L):
+            p.append_attend(layer, k[layer], v[layer], q[layer], out[layer])
+
     def inputs():
         return (torch.randn(qb.shape, device=gpu, generator=gen),
                 torch.randn(kb.shape, device=gpu, generator=gen),
@@ -185,11 +194,11 @@ def test_pager_step_graph_replay(gpu, attend):
         kb.copy_(k)
         vb.copy_(v)
         if s == 0:
-            layers(graph_p, qb, kb, vb, out_g)
+            layers_g(graph_p, qb, kb, vb, out_g)
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                layers(graph_p, qb, kb, vb, out_g)
+                layers_g(graph_p, qb, kb, vb, out_g)
         else:
             out_g.fill_(float("nan"))
             graph.replay()
