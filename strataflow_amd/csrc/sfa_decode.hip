@@ -2205,9 +2205,11 @@ __global__ __launch_bounds__(256) void decode_merge_batch_small_kernel(DecodePar
         for (int i = 0; i < SPT; ++i)
             o[i] = *reinterpret_cast<const floatx4 *>(pg + (int64_t)min(grp + NG * i, S - 1) * sstride + 4 * dc);
     };
+    // the plan's inputs first: the plan is worked out while the guessed
+    // records are in flight
+    const PlanRaw raw = plan_load(p, lane);
     const int rec_g = b * p.guess_splits;  // the guess stays inside the row
     load(rec_g, p.guess_splits);
-    const PlanRaw raw = plan_load(p, lane);
     SlotPlan sp;
     plan_lanes(p, raw, 0, b, lane, sp);
     const int n_active = __builtin_amdgcn_readfirstlane(sp.n_b);
