@@ -366,9 +366,9 @@ struct MoeParams {
 };
 
 // chunks of 8 a lane loads before it uses any in the F16 gate/up product;
-// the F16 kernel is built for four waves per SIMD so that the compiler keeps
-// them all in flight (the launch has 28672 waves for Mixtral's two slots, so
-// the chip stays full)
+// that kernel may take the registers of four waves per SIMD (it takes those
+// of three), so the compiler keeps them all in flight (the launch has 28672
+// waves for Mixtral's two slots, so the chip stays full)
 constexpr int kGateUpBatch = 8;
 
 // act[t][j][f] = silu(gate[e][f] . x[t]) * (up[e][f] . x[t]), e = ids[t][j];
