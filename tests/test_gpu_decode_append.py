@@ -186,3 +186,24 @@ def test_pager_append_attend_equals_two_calls(gpu, attend, kv_type):
         assert torch.equal(oa.view(torch.int32), ob.view(torch.int32)), f"step {s}"
     pa.close()
     pb.close()
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_decode_append_sweep(gpu, oracle_mod, case):
+    # seeded random shapes, page sizes, batches, window starts and cache types:
+    # the fused call against append-then-decode, bit for bit
+    rng = np.random.default_rng(1000 + case)
+    Hq, Hkv, hd = [(32, 8, 128), (8, 2, 64), (16, 4, 128), (8, 8, 32), (16, 2, 64)][case % 5]
+    ps = int(rng.choice([32, 64, 128, 256]))
+    B = int(rng.integers(1, 7))
+    seq = rng.integers(1, 1500, B)
+    seq[rng.random(B) < 0.15] = 0
+    lo = None
+    if case % 3 == 1:
+        lo = [int(rng.integers(0, max(int(n), 1))) for n in seq]
+    kv_type = [1, 0][case % 2]
+    c = Case(oracle_mod, seq_lens=seq, kv_lo=lo, n_head=Hq, n_head_kv=Hkv, head_dim=hd, page_size=ps,
+             seed=case, n_layer=2, kv_type=kv_type)
+    k, v = _new_tokens(gpu, c.B, Hkv, hd, 2000 + case)
+    out0, out1 = _unfused_vs_fused(c, k, v, max(int(seq.max()), 1))
+    _assert_same(c, out0, out1, f"case {case}: {(Hq, Hkv, hd)} ps {ps} seq {seq.tolist()} lo {lo}")
